@@ -1,0 +1,162 @@
+#!/usr/bin/env python3
+"""MXFP4 MoE layer benchmark on one MI355X.
+
+A step is one call of the MoE layer (gptoss_moe_forward: router, top-k,
+routing, MLP1 + SwiGLU, MLP2, weighted top-k reduction) on one batch of
+synthetic tokens of the workload's shape, with inputs and weights resident
+in HBM.  Steps rotate over several copies of the layer's weights so the
+256 MB MALL cannot hold them between steps.
+
+Prints one JSON line: tokens/s, the roofline of the dominant kernel (MLP1
+grouped GEMM) measured with HIP events on the launch stream, the whole-layer
+HBM fraction, and the CPU baseline (the reference CPU engine's MoE block,
+restated in oracle/, timed on this host on a bounded token sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gpt-oss_amd"))
+
+METRIC = "MXFP4 MoE layer tokens/s + % of HBM/MFMA roofline, 20B shape, 1×MI355X"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c1_20b_decode")
+    ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-iters", type=int, default=20)
+    return ap.parse_args()
+
+
+def cpu_baseline(d, budget_s: float) -> dict:
+    """The reference CPU engine's MoE block (run.cpp:657-748, OpenMP matmul)
+    restated in oracle/, one token at a time, on a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+    from synth import bf16_to_f32
+
+    eng = oracle.Fp32Engine(d)
+    x = bf16_to_f32(d.x)
+    eng.token(x[0])  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while n < d.cfg.tokens and time.perf_counter() - t0 < budget_s:
+        eng.token(x[n])
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"{n} of {d.cfg.tokens} tokens of {d.cfg.name}, one token at a time "
+                      f"(run.cpp:657-748 restated, fp32 weights = exact MXFP4 dequant), {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import gptoss_moe
+    import synth
+
+    dev = torch.device("cuda:0")
+    d = synth.make_data(args.config)
+    c = d.cfg
+    layer_bytes = d.weight_bytes
+    copies = args.copies or max(2, min(8, int(np.ceil(1.2e9 / layer_bytes))))
+    base = gptoss_moe.MoeLayer.from_numpy(d, device=dev)
+    layers = [base]
+    for _ in range(copies - 1):
+        w = {k: v.clone() for k, v in base.tensors.items()}
+        layers.append(gptoss_moe.MoeLayer(base.shape, w, c.tokens, dev))
+    x = torch.from_numpy(d.x.view(np.int16)).to(dev)
+    fi = None if d.forced_i is None else torch.from_numpy(d.forced_i).to(dev)
+    fw = None if d.forced_w is None else torch.from_numpy(d.forced_w.view(np.int16)).to(dev)
+    out = torch.empty_like(x)
+
+    for i in range(args.warmup):
+        layers[i % copies].forward(x, out, fi, fw)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        layers[i % copies].forward(x, out, fi, fw)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ev0.elapsed_time(ev1) / args.steps
+
+    # per-kernel durations (HIP events between kernels on the launch stream)
+    prof = {k: [] for k in gptoss_moe.MoeLayer.KERNELS}
+    for i in range(args.profile_iters):
+        r = layers[i % copies].forward_profiled(x, out, fi, fw)
+        for k, v in r.items():
+            prof[k].append(v)
+    kms = {k: statistics.median(v) for k, v in prof.items()}
+
+    counts = layers[(args.profile_iters - 1) % copies].views(c.tokens)["counts"]
+    active = int((counts > 0).sum())
+    pairs = int(counts.sum())
+    alg_bytes = synth.algorithmic_bytes(c, active)
+    flops = synth.algorithmic_flops(c, pairs)
+    # MLP1 algorithmic bytes: active experts' W1 nibbles + scales + b1, x rows in, act rows out
+    H, D = c.hidden, c.intermediate
+    mlp1_bytes = active * (2 * D * H // 2 + 2 * D * H // 32 + 2 * 2 * D) + 2 * c.tokens * H + \
+        2 * pairs * D
+    mlp1_gbs = mlp1_bytes / (kms["mlp1"] * 1e-3) / 1e9
+    tok_s = c.tokens / (ms * 1e-3)
+    res = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random MXFP4 weights, bf16 activations)",
+        "config": {"workload": c.name, "hidden": H, "intermediate": D, "n_experts": c.n_experts,
+                   "top_k": c.top_k, "tokens": c.tokens, "routing": c.routing,
+                   "weight_copies_rotated": copies},
+        "roofline": {"bound": "hbm", "kernel": "grouped_gemm_kernel<mlp1>",
+                     "achieved": round(mlp1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": mlp1_bytes,
+                     "avg_launch_ms": round(kms["mlp1"], 5)},
+        "layer": {"algorithmic_bytes": alg_bytes, "hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
+                  "hbm_frac": round(alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                  "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                  "active_experts": active, "pairs": pairs},
+        "kernel_ms": {k: round(v, 5) for k, v in kms.items()},
+        "wall_s_timed": round(wall, 4),
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

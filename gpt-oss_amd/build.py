@@ -1,0 +1,36 @@
+"""Build libgptoss_moe.so in-tree for gfx950 (hipcc, no JIT cache)."""
+from __future__ import annotations
+
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in any kernel.
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-munsafe-fp-atomics", "-Wall", "-Wno-unused-variable",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"),
+]
+
+SOURCES = [os.path.join(HERE, "csrc", "gptoss_moe.hip")]
+LIB = os.path.join(HERE, "libgptoss_moe.so")
+
+
+def build(verbose: bool = False) -> str:
+    cmd = [HIPCC, *HIP_FLAGS, *SOURCES, "-o", LIB]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
+                     if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{msgs}")
+    if verbose and msgs.strip():
+        print(msgs)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

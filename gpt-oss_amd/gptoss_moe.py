@@ -1,0 +1,266 @@
+"""Host-side mirror of the reference's MoE entry point over the C ABI in
+include/gptoss_moe.h (libgptoss_moe.so, built from csrc/gptoss_moe.hip).
+
+`MoeLayer` plays the role of moe_gpu (getp-csrc/getp_run.cpp:2540): it owns
+one layer's device weights and a workspace and runs the layer on a HIP
+stream.  Tensors are torch CUDA (HIP) tensors used only as device memory;
+bf16 data is held as int16/uint16 bit patterns or torch.bfloat16.
+
+There is no fallback: if the shared library is missing or a call fails, the
+call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgptoss_moe.so")
+
+OK = 0
+ERR_INVALID_ARG = -1
+ERR_WORKSPACE = -2
+ERR_HIP = -3
+ERR_UNSUPPORTED = -4
+FLAG_RESIDUAL_ADD = 1
+
+_ERRNAMES = {ERR_INVALID_ARG: "invalid argument", ERR_WORKSPACE: "workspace too small",
+             ERR_HIP: "HIP error", ERR_UNSUPPORTED: "unsupported shape"}
+
+
+class MoeError(RuntimeError):
+    def __init__(self, fn: str, rc: int, hip: int = 0):
+        super().__init__(f"{fn} failed: {rc} ({_ERRNAMES.get(rc, '?')})"
+                         + (f", hipError {hip}" if rc == ERR_HIP else ""))
+        self.rc = rc
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("intermediate", ctypes.c_int),
+                ("n_experts", ctypes.c_int), ("top_k", ctypes.c_int),
+                ("swiglu_limit", ctypes.c_float), ("swiglu_alpha", ctypes.c_float)]
+
+
+class Weights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("router_w", "router_b", "w1", "w1_scales", "b1", "w2", "w2_scales", "b2")]
+
+
+class Views(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("logits", "topk_i", "topk_w", "counts", "offsets", "local_ids", "row_token",
+                 "row_weight", "row_slot", "act", "slots", "status")]
+
+
+_VP = ctypes.c_void_p
+_SIGS = {
+    "gptoss_moe_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Shape), ctypes.c_int]),
+    "gptoss_moe_workspace_init": (ctypes.c_int, [_VP, ctypes.c_size_t, _VP]),
+    "gptoss_moe_workspace_views": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.c_int, _VP,
+                                                  ctypes.c_size_t, ctypes.POINTER(Views)]),
+    "gptoss_moe_forward": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights), _VP, _VP,
+                                          ctypes.c_int, _VP, _VP, ctypes.c_uint, _VP,
+                                          ctypes.c_size_t, ctypes.c_int, _VP]),
+    "gptoss_moe_route": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights), _VP,
+                                        ctypes.c_int, _VP, _VP, _VP, ctypes.c_size_t,
+                                        ctypes.c_int, _VP]),
+    "gptoss_moe_layer": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights), _VP, _VP,
+                                        _VP, ctypes.c_int, _VP, ctypes.c_size_t, ctypes.c_int,
+                                        _VP]),
+    "gptoss_moe_forward_profiled": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights),
+                                                   _VP, _VP, ctypes.c_int, _VP, _VP,
+                                                   ctypes.c_uint, _VP, ctypes.c_size_t,
+                                                   ctypes.c_int, _VP,
+                                                   ctypes.POINTER(ctypes.c_float)]),
+    "gptoss_moe_rmsnorm": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
+    "gptoss_moe_dequant_mxfp4": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int64,
+                                                ctypes.c_int64, _VP, _VP]),
+    "gptoss_moe_last_hip_error": (ctypes.c_int, []),
+    "gptoss_moe_version": (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libgptoss_moe.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(fn: str, rc: int) -> None:
+    if rc != OK:
+        raise MoeError(fn, rc, load_library().gptoss_moe_last_hip_error())
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def make_shape(hidden, intermediate, n_experts, top_k, limit=7.0, alpha=1.702) -> Shape:
+    return Shape(hidden, intermediate, n_experts, top_k, limit, alpha)
+
+
+def workspace_size(shape: Shape, max_tokens: int) -> int:
+    return load_library().gptoss_moe_workspace_size(ctypes.byref(shape), max_tokens)
+
+
+class MoeLayer:
+    """One MoE layer resident on a GPU: weights, workspace and entry points.
+
+    Weights are torch uint8/int16 CUDA tensors in the layouts of
+    include/gptoss_moe.h.  `max_tokens` sizes the workspace.
+    """
+
+    def __init__(self, shape: Shape, weights: dict, max_tokens: int, device="cuda"):
+        import torch
+        self.lib = load_library()
+        self.shape = shape
+        self.max_tokens = int(max_tokens)
+        self.device = torch.device(device)
+        self.tensors = dict(weights)  # keep device buffers alive
+        self.w = Weights(*[_ptr(self.tensors.get(n)) for n, _ in Weights._fields_])
+        self.ws_bytes = workspace_size(shape, self.max_tokens)
+        if self.ws_bytes == 0:
+            raise MoeError("gptoss_moe_workspace_size", ERR_INVALID_ARG)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=self.device)
+        _check("gptoss_moe_workspace_init",
+               self.lib.gptoss_moe_workspace_init(self.ws.data_ptr(), self.ws_bytes, _stream()))
+
+    @classmethod
+    def from_numpy(cls, d, max_tokens: Optional[int] = None, device="cuda") -> "MoeLayer":
+        """Upload a synth.MoeData layer."""
+        import torch
+        c = d.cfg
+        dev = torch.device(device)
+
+        def up(a):
+            a = np.ascontiguousarray(a)
+            if a.dtype == np.uint16:
+                a = a.view(np.int16)
+            return torch.from_numpy(a).to(dev)
+
+        w = {"router_w": up(d.router_w), "router_b": up(d.router_b), "w1": up(d.w1),
+             "w1_scales": up(d.s1), "b1": up(d.b1), "w2": up(d.w2), "w2_scales": up(d.s2),
+             "b2": up(d.b2)}
+        shape = make_shape(c.hidden, c.intermediate, c.n_experts, c.top_k)
+        return cls(shape, w, max_tokens or c.tokens, device)
+
+    # -- entry points ---------------------------------------------------
+    def forward(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,
+                stream=None):
+        """e_agg (or out + e_agg with residual=True) for bf16 rows x_norm [T][H]."""
+        import torch
+        T = x_norm.shape[0]
+        if out is None:
+            out = torch.empty_like(x_norm)
+        rc = self.lib.gptoss_moe_forward(
+            ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(x_norm), _ptr(out), T,
+            _ptr(forced_i), _ptr(forced_w), FLAG_RESIDUAL_ADD if residual else 0,
+            self.ws.data_ptr(), self.ws_bytes, self.max_tokens, _stream(stream))
+        _check("gptoss_moe_forward", rc)
+        return out
+
+    KERNELS = ("route", "index", "mlp1", "mlp2", "finalize")
+
+    def forward_profiled(self, x_norm, out, forced_i=None, forced_w=None, stream=None) -> dict:
+        """forward() with per-kernel HIP-event durations (ms); synchronises."""
+        ms = (ctypes.c_float * 5)()
+        rc = self.lib.gptoss_moe_forward_profiled(
+            ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(x_norm), _ptr(out),
+            x_norm.shape[0], _ptr(forced_i), _ptr(forced_w), 0, self.ws.data_ptr(),
+            self.ws_bytes, self.max_tokens, _stream(stream), ms)
+        _check("gptoss_moe_forward_profiled", rc)
+        return dict(zip(self.KERNELS, list(ms)))
+
+    def route(self, x_norm, forced_i=None, forced_w=None, stream=None):
+        rc = self.lib.gptoss_moe_route(
+            ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(x_norm), x_norm.shape[0],
+            _ptr(forced_i), _ptr(forced_w), self.ws.data_ptr(), self.ws_bytes, self.max_tokens,
+            _stream(stream))
+        _check("gptoss_moe_route", rc)
+
+    def layer(self, x, rms_w, t_scratch=None, stream=None):
+        """moe_gpu at TP = 1: x += MoE(RMSNorm(x)) in place."""
+        import torch
+        if t_scratch is None:
+            t_scratch = torch.empty_like(x)
+        rc = self.lib.gptoss_moe_layer(
+            ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(rms_w), _ptr(x), _ptr(t_scratch),
+            x.shape[0], self.ws.data_ptr(), self.ws_bytes, self.max_tokens, _stream(stream))
+        _check("gptoss_moe_layer", rc)
+        return x
+
+    def views(self, n_tokens: int) -> dict:
+        """Workspace contents of the last call (copied to host numpy)."""
+        import torch
+        v = Views()
+        _check("gptoss_moe_workspace_views", self.lib.gptoss_moe_workspace_views(
+            ctypes.byref(self.shape), self.max_tokens, self.ws.data_ptr(), self.ws_bytes,
+            ctypes.byref(v)))
+        base = self.ws.data_ptr()
+        E, K, D, H = (self.shape.n_experts, self.shape.top_k, self.shape.intermediate,
+                      self.shape.hidden)
+        T = n_tokens
+        torch.cuda.current_stream().synchronize()
+
+        def grab(ptr, count, dtype, esize):
+            off = ptr - base
+            raw = self.ws[off: off + count * esize].cpu().numpy()
+            return raw.view(dtype)
+
+        offsets = grab(v.offsets, E + 1, np.int32, 4).copy()
+        P = int(offsets[E])
+        return {
+            "logits": grab(v.logits, T * E, np.uint16, 2).reshape(T, E),
+            "topk_i": grab(v.topk_i, T * K, np.int32, 4).reshape(T, K),
+            "topk_w": grab(v.topk_w, T * K, np.uint16, 2).reshape(T, K),
+            "counts": grab(v.counts, E, np.int32, 4),
+            "offsets": offsets,
+            "local_ids": grab(v.local_ids, T * K, np.int32, 4).reshape(T, K),
+            "row_token": grab(v.row_token, P, np.int32, 4),
+            "row_weight": grab(v.row_weight, P, np.float32, 4),
+            "row_slot": grab(v.row_slot, P, np.int32, 4),
+            "act": grab(v.act, P * D, np.uint16, 2).reshape(P, D),
+            "slots": grab(v.slots, T * K * H, np.uint16, 2).reshape(T, K, H),
+            "status": grab(v.status, 4, np.int32, 4),
+        }
+
+
+def rmsnorm(x, weight, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty_like(x)
+    rc = load_library().gptoss_moe_rmsnorm(_ptr(x), _ptr(weight), _ptr(out), x.shape[0],
+                                           x.shape[1], _stream(stream))
+    _check("gptoss_moe_rmsnorm", rc)
+    return out
+
+
+def dequant_mxfp4(packed, scales, n_experts: int, n_rows: int, k_cols: int, stream=None):
+    """MXFP4 -> bf16 (int16 bit patterns) [E][n_rows*k_cols]."""
+    import torch
+    out = torch.empty((n_experts, n_rows * k_cols), dtype=torch.int16, device=packed.device)
+    rc = load_library().gptoss_moe_dequant_mxfp4(_ptr(packed), _ptr(scales), n_experts, n_rows,
+                                                 k_cols, _ptr(out), _stream(stream))
+    _check("gptoss_moe_dequant_mxfp4", rc)
+    return out

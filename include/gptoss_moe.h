@@ -1,0 +1,170 @@
+/*
+ * gptoss_moe.h — C ABI of the MI355X (gfx950) MXFP4 mixture-of-experts layer.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream, and
+ * returns an int status (0 = ok, negative = error).  Nothing here exits or
+ * aborts, and no call allocates device memory: the caller owns weights,
+ * activations and the workspace.  All work is stream-ordered on `stream`;
+ * no entry point synchronises the host with the device.
+ *
+ * Buffer layouts are those of the reference's 120B MXFP4 weights
+ * (getp-csrc/getp_run.cpp:704-721, :1036-1049, memory/mxfp4.hpp:42-57):
+ *   - MXFP4 weight of expert e, logical [N][K] (row-major, out x in), flattened:
+ *       element i = n*K + k lives in byte  e*(N*K/2) + i/2,
+ *       low nibble = even i, high nibble = odd i (E2M1 code, bit 3 = sign);
+ *       its e8m0 scale is byte            e*(N*K/32) + i/32,
+ *       value = E2M1(code) * 2^(scale-127)  (scale byte 0 -> 0.0, 255 -> +Inf).
+ *   - MLP1: N = 2*D (row 2j = gate j, row 2j+1 = up j), K = H.
+ *   - MLP2: N = H, K = D.
+ *   - bf16 values are passed as uint16_t bit patterns.
+ */
+#ifndef GPTOSS_MOE_H
+#define GPTOSS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define GPTOSS_MOE_OK 0
+#define GPTOSS_MOE_ERR_INVALID_ARG (-1)     /* bad shape, null pointer, bad flag */
+#define GPTOSS_MOE_ERR_WORKSPACE (-2)       /* workspace too small or misaligned */
+#define GPTOSS_MOE_ERR_HIP (-3)             /* a HIP call failed; see gptoss_moe_last_hip_error */
+#define GPTOSS_MOE_ERR_UNSUPPORTED (-4)     /* shape outside the supported envelope */
+
+/* ---- forward flags ----------------------------------------------------- */
+/* out[t][h] = bf16(out[t][h] + e_agg[t][h]) instead of out = e_agg
+ * (the residual update of other_kernels.hpp:17-35). */
+#define GPTOSS_MOE_FLAG_RESIDUAL_ADD 1u
+
+/* Shape of one MoE layer (run.cpp:25-45 Config fields). */
+typedef struct gptoss_moe_shape {
+    int hidden;        /* H = Config.hidden_dim; multiple of 32 */
+    int intermediate;  /* D = Config.intermediate_dim; multiple of 32 */
+    int n_experts;     /* E = Config.n_experts; 1..256 */
+    int top_k;         /* k = Config.experts_per_token; 1..8, <= E */
+    float swiglu_limit; /* Config.swiglu_limit (7.0 for gpt-oss) */
+    float swiglu_alpha; /* 1.702 for gpt-oss (moe.hpp:1472-1496 caller) */
+} gptoss_moe_shape;
+
+/* One layer's MoE weights (GPUTransformerWeights MoE fields,
+ * getp_run.cpp:65-77, at one layer offset).  All device pointers. */
+typedef struct gptoss_moe_weights {
+    const uint16_t *router_w;  /* bf16 [E][H] (w_router, used as out x in) */
+    const uint16_t *router_b;  /* bf16 [E] */
+    const uint8_t *w1;         /* MXFP4 nibbles, E * (2D*H/2) bytes */
+    const uint8_t *w1_scales;  /* e8m0, E * (2D*H/32) bytes */
+    const uint16_t *b1;        /* bf16 [E][2D] */
+    const uint8_t *w2;         /* MXFP4 nibbles, E * (H*D/2) bytes */
+    const uint8_t *w2_scales;  /* e8m0, E * (H*D/32) bytes */
+    const uint16_t *b2;        /* bf16 [E][H] */
+} gptoss_moe_weights;
+
+/* Views into a workspace after a call, for inspection and parity tests.
+ * Filled by gptoss_moe_workspace_views; all device pointers. */
+typedef struct gptoss_moe_views {
+    uint16_t *logits;     /* bf16 [T][E] router logits (no bias) */
+    int32_t *topk_i;      /* [T][k] selected experts, descending score order */
+    uint16_t *topk_w;     /* bf16 [T][k] softmax weights over the k selected */
+    int32_t *counts;      /* [E] tokens routed to each expert */
+    int32_t *offsets;     /* [E+1] exclusive prefix of counts */
+    int32_t *local_ids;   /* [T][k] compact row of (t, slot), -1 if dropped */
+    int32_t *row_token;   /* [T*k] compact row -> token (token-ascending per expert) */
+    float *row_weight;    /* [T*k] compact row -> router weight */
+    int32_t *row_slot;    /* [T*k] compact row -> token-order slot t*k + j */
+    uint16_t *act;        /* bf16 [T*k][D] SwiGLU output rows (MLP2 input) */
+    uint16_t *slots;      /* bf16 [T][k][H] MLP2 outputs scattered to token order */
+    int32_t *status;      /* [4] device flags: [0] = dropped-slot count */
+} gptoss_moe_views;
+
+/* Bytes of workspace a call with up to max_tokens tokens needs. */
+size_t gptoss_moe_workspace_size(const gptoss_moe_shape *shape, int max_tokens);
+
+/* Zero a fresh workspace once before its first use (stream-ordered). */
+int gptoss_moe_workspace_init(void *workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Pointers into `workspace` laid out for (shape, max_tokens). */
+int gptoss_moe_workspace_views(const gptoss_moe_shape *shape, int max_tokens,
+                               void *workspace, size_t ws_bytes,
+                               gptoss_moe_views *views);
+
+/*
+ * The MoE layer on normalised activations: replaces moe_gpu's steps 2-8
+ * (getp_run.cpp:2609-2830): router GEMM, top-k + softmax
+ * (moe.hpp:465-599), expert histogram + prefix + row map (moe.hpp:744-760,
+ * :1173-1270, getp_run.cpp:2639-2692), gather (moe.hpp:983-1048), MLP1 +
+ * bias (moe.hpp:2651-2913), clamped SwiGLU (moe.hpp:1472-1496), MLP2 + bias
+ * (moe.hpp:2923-3185) and the weighted top-k reduction (moe.hpp:700-730).
+ *
+ *   x_norm   bf16 [T][H]  input rows (device)
+ *   out      bf16 [T][H]  e_agg, or the residual stream with FLAG_RESIDUAL_ADD
+ *   forced_topk_i / forced_topk_w: optional [T][k] int32 / bf16 routing that
+ *            replaces the router (both NULL = use the router).  Indices must
+ *            be distinct per token and in [0, E); an out-of-range slot is
+ *            dropped and counted in views.status[0].
+ * `max_tokens` is the value the workspace was sized for.
+ */
+int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                       const uint16_t *x_norm, uint16_t *out, int n_tokens,
+                       const int32_t *forced_topk_i, const uint16_t *forced_topk_w,
+                       unsigned flags, void *workspace, size_t ws_bytes, int max_tokens,
+                       hipStream_t stream);
+
+/*
+ * Routing only (router GEMM, top-k + softmax, histogram, prefix, row map):
+ * the first half of gptoss_moe_forward, leaving its results in the workspace
+ * (see gptoss_moe_workspace_views).  Replaces getp_run.cpp:2609-2732.
+ */
+int gptoss_moe_route(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                     const uint16_t *x_norm, int n_tokens,
+                     const int32_t *forced_topk_i, const uint16_t *forced_topk_w,
+                     void *workspace, size_t ws_bytes, int max_tokens, hipStream_t stream);
+
+/*
+ * Whole moe_gpu layer at one GPU (getp_run.cpp:2540-2887 with TP = 1):
+ * t = RMSNorm(x; rms_w) (rmsnorm.hpp:113-164), then the MoE of
+ * gptoss_moe_forward on t, then x = bf16(x + e_agg) in place
+ * (other_kernels.hpp:17-35).  `t_scratch` is a caller buffer bf16 [T][H].
+ */
+int gptoss_moe_layer(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                     const uint16_t *rms_w, uint16_t *x, uint16_t *t_scratch, int n_tokens,
+                     void *workspace, size_t ws_bytes, int max_tokens, hipStream_t stream);
+
+/*
+ * Instrumentation (no counterpart in the reference): gptoss_moe_forward with
+ * a HIP event recorded on `stream` between its kernels; waits for the last
+ * event and writes the five kernel durations in ms to kernel_ms[0..4]
+ * (route, index, mlp1, mlp2, finalize).  Synchronises the host.
+ */
+int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                                const uint16_t *x_norm, uint16_t *out, int n_tokens,
+                                const int32_t *forced_topk_i, const uint16_t *forced_topk_w,
+                                unsigned flags, void *workspace, size_t ws_bytes, int max_tokens,
+                                hipStream_t stream, float *kernel_ms);
+
+/* RMSNorm rows: out = bf16(w * (x * rsqrt(mean(x^2) + 1e-5))), with the sum
+ * of squares in double (rmsnorm.hpp:113-164). */
+int gptoss_moe_rmsnorm(const uint16_t *x, const uint16_t *weight, uint16_t *out,
+                       int n_rows, int size, hipStream_t stream);
+
+/* MXFP4 -> bf16 dequantisation of n_experts segments of N*K elements each
+ * (dequant_mxfp4_pairs_to_bf16_kernel, memory/mxfp4.hpp:223-275), using the
+ * same conversion the GEMMs use.  out: bf16 [E][N*K]. */
+int gptoss_moe_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int n_experts,
+                             int64_t n_rows, int64_t k_cols, uint16_t *out,
+                             hipStream_t stream);
+
+/* Last HIP error seen by this library on the calling thread (hipError_t). */
+int gptoss_moe_last_hip_error(void);
+
+/* Library version string. */
+const char *gptoss_moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GPTOSS_MOE_H */

@@ -1,0 +1,509 @@
+/*
+ * moe_oracle.c — CPU restatement of the reference's MXFP4 MoE layer.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the parity tests, the
+ * smoke check and bench.py's cpu_baseline leg compare the HIP path against.
+ * The product (gpt-oss_amd/) never links, loads or calls it.
+ *
+ * Two semantics are restated:
+ *   (i)  "getp" — the reference GPU batch path at TP = 1
+ *        (getp-csrc/getp_run.cpp:2540-2887), with bf16 rounding at the same
+ *        points: router logits bf16, scores fp32 = logit + bias, top-k with
+ *        the epsilon tie rule, softmax weights bf16, MLP1 out bf16,
+ *        SwiGLU out bf16, MLP2 out bf16, weighted reduction fp32 -> bf16.
+ *        Dot products are accumulated in double (the exact limit of the
+ *        reference's fp32 MFMA accumulation, whose internal order is not
+ *        specified), except the router GEMM, whose fp32 order is pinned
+ *        (see orc_router_logits).
+ *   (ii) "fp32" — the CPU engine's MoE block (run.cpp:657-748), used as the
+ *        CPU baseline that bench.py times (OpenMP over output rows, as
+ *        run.cpp:355-368).
+ *
+ * Build: see oracle/Makefile (-ffp-contract=off: every fused multiply-add
+ * here is an explicit fmaf()).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------------------------------------------------------------- bf16 -- */
+
+/* fp32 -> bf16, round to nearest even; NaN -> quiet NaN (sign kept).
+ * Matches __float2bfloat16 / pack2_bf16_bits_f32 (matmul.hpp:144-148). */
+uint16_t orc_f2bf(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float orc_bf2f(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* -------------------------------------------------------------- MXFP4 -- */
+
+/* E2M1 magnitudes, memory/mxfp4.hpp:7-10 (== FP4_VALUES in
+ * export_model_bin/gpt-oss-20b/export_model_bin.py:66-83). */
+static const float kE2M1[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+/* Scale X = 2^(e-127) by placing e in the fp32 exponent field
+ * (mxfp4.hpp:53: __uint_as_float(uint32_t(e) << 23)); e = 0 gives 0.0. */
+float orc_e8m0_to_f32(uint8_t e) {
+    uint32_t u = (uint32_t)e << 23;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Element i of one segment (mxfp4.hpp:42-57): byte i>>1, low nibble for even
+ * i (export_model_bin.py:112-117), scale i>>5, value = code * X in fp32. */
+float orc_mxfp4_elem(const uint8_t *packed, const uint8_t *scales, int64_t i) {
+    uint8_t byte = packed[i >> 1];
+    uint8_t nib = (uint8_t)((byte >> ((i & 1) << 2)) & 0xF);
+    return kE2M1[nib] * orc_e8m0_to_f32(scales[i >> 5]);
+}
+
+/* One segment of n elements -> bf16 (dequant_mxfp4_pairs_to_bf16_kernel,
+ * mxfp4.hpp:223-275). */
+void orc_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int64_t n, uint16_t *out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f2bf(orc_mxfp4_elem(packed, scales, i));
+}
+
+/* Same, to fp32 (the CPU engine's dequantised weights). */
+void orc_dequant_mxfp4_f32(const uint8_t *packed, const uint8_t *scales, int64_t n, float *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_mxfp4_elem(packed, scales, i);
+}
+
+/* ------------------------------------------------------------- router -- */
+
+/*
+ * Router logits, logits[t][e] = bf16(sum_k x[t][k] * wr[e][k]) with fp32
+ * accumulation and no bias (matmul_vec128_singlebuf_Abf16, matmul.hpp:1344,
+ * called at getp_run.cpp:2612-2620).  The reference accumulates inside MFMA
+ * tiles in an unspecified order; this build pins one fp32 order so router
+ * indices can be compared bit for bit: 64 partial sums p[l], each a chain of
+ * fmaf over k = 512*i + 8*l + j (i ascending, then j = 0..7), then a
+ * butterfly p[l] = p[l] + p[l ^ s] for s = 32, 16, 8, 4, 2, 1.
+ * H must be a multiple of 8.
+ */
+void orc_router_logits(const uint16_t *x, const uint16_t *wr, int T, int H, int E,
+                       uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; ++t) {
+        float p[64], q[64];
+        for (int e = 0; e < E; ++e) {
+            const uint16_t *xr = x + (int64_t)t * H;
+            const uint16_t *wrow = wr + (int64_t)e * H;
+            for (int l = 0; l < 64; ++l) {
+                float acc = 0.0f;
+                for (int base = 8 * l; base < H; base += 512)
+                    for (int j = 0; j < 8; ++j)
+                        acc = fmaf(orc_bf2f(xr[base + j]), orc_bf2f(wrow[base + j]), acc);
+                p[l] = acc;
+            }
+            for (int s = 32; s >= 1; s >>= 1) {
+                for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ s];
+                memcpy(p, q, sizeof(p));
+            }
+            out[(int64_t)t * E + e] = orc_f2bf(p[0]);
+        }
+    }
+}
+
+/* ---------------------------------------------------------- top-k ------ */
+
+typedef struct {
+    float v;
+    int i;
+} orc_pick;
+
+/* better_pick (moe.hpp:333-342): larger wins unless within eps*max(|a|,|b|),
+ * then the lower index wins. */
+static int orc_better(orc_pick a, orc_pick b, float eps) {
+    float thr = eps * fmaxf(fabsf(a.v), fabsf(b.v));
+    if (a.v > b.v + thr) return 1;
+    if (fabsf(a.v - b.v) <= thr && a.i < b.i) return 1;
+    return 0;
+}
+
+/*
+ * route_select_softmax_kernel_bf16io + run_route_select_softmax_fused
+ * (moe.hpp:465-599) for one token: scores fp32 = logit + bias, K rounds of a
+ * block arg-max over nthreads = clamp(nextpow2(E), 64, 512) threads (thread
+ * tid scans i = tid, tid + nthreads, ...; then a halving tree), softmax over
+ * the K selected (expf, 1/(sum + 1e-20)), weights rounded to bf16.  The
+ * reference only instantiates K = 4; the same rule is used for any K <= 8.
+ * A round that finds no finite candidate yields index -1 (the reference
+ * writes E there).
+ */
+void orc_topk_softmax(const uint16_t *logits, const uint16_t *bias, int T, int E, int K,
+                      int32_t *topk_i, uint16_t *topk_w) {
+    int nthreads = 1;
+    while (nthreads < E) nthreads <<= 1;
+    if (nthreads < 64) nthreads = 64;
+    if (nthreads > 512) nthreads = 512;
+    const float eps = 1e-6f;
+    orc_pick *red = (orc_pick *)malloc(sizeof(orc_pick) * nthreads);
+    float *sc = (float *)malloc(sizeof(float) * E);
+    unsigned char *vis = (unsigned char *)malloc(E);
+    for (int t = 0; t < T; ++t) {
+        for (int i = 0; i < E; ++i) {
+            sc[i] = orc_bf2f(logits[(int64_t)t * E + i]) + orc_bf2f(bias[i]);
+            vis[i] = 0;
+        }
+        int sel_i[8] = {0};
+        float sel_v[8] = {0};
+        for (int s = 0; s < K; ++s) {
+            for (int tid = 0; tid < nthreads; ++tid) {
+                orc_pick best = {-INFINITY, E};
+                for (int i = tid; i < E; i += nthreads) {
+                    if (vis[i]) continue;
+                    orc_pick c = {sc[i], i};
+                    if (orc_better(c, best, eps)) best = c;
+                }
+                red[tid] = best;
+            }
+            for (int st = nthreads >> 1; st > 0; st >>= 1)
+                for (int tid = 0; tid < st; ++tid)
+                    if (orc_better(red[tid + st], red[tid], eps)) red[tid] = red[tid + st];
+            sel_i[s] = red[0].i;
+            sel_v[s] = red[0].v;
+            if (red[0].i < E) vis[red[0].i] = 1;
+        }
+        float mx = sel_v[0];
+        for (int s = 1; s < K; ++s) mx = fmaxf(mx, sel_v[s]);
+        float ex[8], sum = 0.0f;
+        for (int s = 0; s < K; ++s) {
+            ex[s] = expf(sel_v[s] - mx);
+            sum += ex[s];
+        }
+        const float inv = 1.0f / (sum + 1e-20f);
+        for (int s = 0; s < K; ++s) {
+            topk_w[(int64_t)t * K + s] = orc_f2bf(ex[s] * inv);
+            topk_i[(int64_t)t * K + s] = sel_i[s] < E ? sel_i[s] : -1;
+        }
+    }
+    free(red);
+    free(sc);
+    free(vis);
+}
+
+/* ----------------------------------------------------- routing index -- */
+
+/* Slot (t, k) is live iff its expert is in [0, E) and not already taken by
+ * an earlier slot of the same token. */
+static int orc_slot_live(const int32_t *ti, int t, int K, int k, int E) {
+    int e = ti[(int64_t)t * K + k];
+    if (e < 0 || e >= E) return 0;
+    for (int j = 0; j < k; ++j)
+        if (ti[(int64_t)t * K + j] == e) return 0;
+    return 1;
+}
+
+/*
+ * Histogram (count_tokens_per_expert_kernel, moe.hpp:744-760), exclusive
+ * prefix (host loop, getp_run.cpp:2651-2657) and the compact row map of
+ * route_build_index_kernel_bf16wts (moe.hpp:1173-1270): rows of expert e are
+ * offsets[e] .. offsets[e+1]-1 in ascending token order.  Returns the number
+ * of dropped (dead) slots.
+ */
+int orc_route_index(const int32_t *ti, const uint16_t *tw, int T, int K, int E, int32_t *counts,
+                    int32_t *offsets, int32_t *local_ids, int32_t *row_token, float *row_w) {
+    int dropped = 0;
+    for (int e = 0; e < E; ++e) counts[e] = 0;
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < K; ++k) {
+            if (orc_slot_live(ti, t, K, k, E))
+                counts[ti[(int64_t)t * K + k]]++;
+            else
+                dropped++;
+        }
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    for (int64_t i = 0; i < (int64_t)T * K; ++i) local_ids[i] = -1;
+    for (int e = 0; e < E; ++e) {
+        int row = offsets[e];
+        for (int t = 0; t < T; ++t)
+            for (int k = 0; k < K; ++k)
+                if (orc_slot_live(ti, t, K, k, E) && ti[(int64_t)t * K + k] == e) {
+                    local_ids[(int64_t)t * K + k] = row;
+                    row_token[row] = t;
+                    row_w[row] = orc_bf2f(tw[(int64_t)t * K + k]);
+                    row++;
+                }
+    }
+    return dropped;
+}
+
+/* ------------------------------------------------------------ experts -- */
+
+static double orc_dot(const float *a, const float *b, int n) {
+    double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int k = 0;
+    for (; k + 8 <= n; k += 8)
+        for (int j = 0; j < 8; ++j) s[j] += (double)a[k + j] * (double)b[k + j];
+    for (; k < n; ++k) s[0] += (double)a[k] * (double)b[k];
+    return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
+/* Clamped SwiGLU of the reference GPU path (moe.hpp:1472-1496): both gate
+ * and up clamped to [-limit, limit], out = g*sigma(alpha*g)*(u+1) as
+ * fmaf(g*sig, u, g*sig).  (The CPU engine clamps the gate only from above,
+ * run.cpp:706-724; see orc_moe_fp32_token.) */
+static float orc_swiglu(float g, float u, float limit, float alpha) {
+    g = fminf(fmaxf(g, -limit), limit);
+    u = fminf(fmaxf(u, -limit), limit);
+    const float sig = 1.0f / (1.0f + expf(-alpha * g));
+    g = g * sig;
+    return fmaf(g, u, g);
+}
+
+/*
+ * Expert MLPs and weighted reduction, getp semantics, for given routing.
+ *   x_norm bf16 [T][H]; weights MXFP4 as in include/gptoss_moe.h.
+ *   e_agg  bf16 [T][H] out.  act bf16 [P][D] out (optional, compact rows).
+ * MLP1 (moe.hpp:2783-2858): bf16(acc + b1); SwiGLU -> bf16; MLP2: bf16(acc +
+ * b2) (TP = 1, getp_run.cpp:951-967); reduction (moe.hpp:700-730): fmaf over
+ * the k slots in slot order, fp32, then bf16.
+ */
+void orc_moe_experts(int H, int D, int E, int K, float limit, float alpha, const uint16_t *x_norm,
+                     const uint8_t *w1, const uint8_t *s1, const uint16_t *b1, const uint8_t *w2,
+                     const uint8_t *s2, const uint16_t *b2, const int32_t *ti, const uint16_t *tw,
+                     int T, uint16_t *e_agg, uint16_t *act_out) {
+    const int N1 = 2 * D;
+    int32_t *counts = (int32_t *)malloc(sizeof(int32_t) * E);
+    int32_t *offsets = (int32_t *)malloc(sizeof(int32_t) * (E + 1));
+    int32_t *local_ids = (int32_t *)malloc(sizeof(int32_t) * (size_t)T * K + 4);
+    int32_t *row_token = (int32_t *)malloc(sizeof(int32_t) * (size_t)T * K + 4);
+    float *row_w = (float *)malloc(sizeof(float) * (size_t)T * K + 4);
+    orc_route_index(ti, tw, T, K, E, counts, offsets, local_ids, row_token, row_w);
+    const int P = offsets[E];
+    uint16_t *y = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)P * H + 2);
+    uint16_t *act = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)P * D + 2);
+    float *xf = (float *)malloc(sizeof(float) * (size_t)T * H);
+    for (int64_t i = 0; i < (int64_t)T * H; ++i) xf[i] = orc_bf2f(x_norm[i]);
+    float *W = (float *)malloc(sizeof(float) * (size_t)N1 * H);
+    float *hrow = (float *)malloc(sizeof(float) * (size_t)(P > 0 ? P : 1) * D);
+    for (int e = 0; e < E; ++e) {
+        const int r0 = offsets[e], nr = counts[e];
+        if (nr == 0) continue;
+        /* MLP1 + SwiGLU */
+        const int64_t seg1 = (int64_t)N1 * H;
+        orc_dequant_mxfp4_f32(w1 + e * (seg1 / 2), s1 + e * (seg1 / 32), seg1, W);
+        for (int r = 0; r < nr; ++r) {
+            const float *xr = xf + (int64_t)row_token[r0 + r] * H;
+#pragma omp parallel for schedule(static)
+            for (int j = 0; j < D; ++j) {
+                float g = (float)orc_dot(W + (int64_t)(2 * j) * H, xr, H);
+                float u = (float)orc_dot(W + (int64_t)(2 * j + 1) * H, xr, H);
+                g = orc_bf2f(orc_f2bf(g + orc_bf2f(b1[(int64_t)e * N1 + 2 * j])));
+                u = orc_bf2f(orc_f2bf(u + orc_bf2f(b1[(int64_t)e * N1 + 2 * j + 1])));
+                uint16_t a = orc_f2bf(orc_swiglu(g, u, limit, alpha));
+                act[(int64_t)(r0 + r) * D + j] = a;
+                hrow[(int64_t)r * D + j] = orc_bf2f(a);
+            }
+        }
+        /* MLP2 */
+        const int64_t seg2 = (int64_t)H * D;
+        orc_dequant_mxfp4_f32(w2 + e * (seg2 / 2), s2 + e * (seg2 / 32), seg2, W);
+        for (int r = 0; r < nr; ++r) {
+#pragma omp parallel for schedule(static)
+            for (int h = 0; h < H; ++h) {
+                float v = (float)orc_dot(W + (int64_t)h * D, hrow + (int64_t)r * D, D);
+                y[(int64_t)(r0 + r) * H + h] = orc_f2bf(v + orc_bf2f(b2[(int64_t)e * H + h]));
+            }
+        }
+    }
+    for (int t = 0; t < T; ++t)
+        for (int h = 0; h < H; ++h) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; ++k) {
+                int ci = local_ids[(int64_t)t * K + k];
+                if (ci >= 0) acc = fmaf(row_w[ci], orc_bf2f(y[(int64_t)ci * H + h]), acc);
+            }
+            e_agg[(int64_t)t * H + h] = orc_f2bf(acc);
+        }
+    if (act_out) memcpy(act_out, act, sizeof(uint16_t) * (size_t)P * D);
+    free(counts); free(offsets); free(local_ids); free(row_token); free(row_w);
+    free(y); free(act); free(xf); free(W); free(hrow);
+}
+
+/* ----------------------------------------------------- layer boundary -- */
+
+/* rmsnorm_kernel_bf16_io (rmsnorm.hpp:113-164) with its 256-thread layout:
+ * per-thread strided double partials, halving tree, inv = 1/sqrt(mean+1e-5)
+ * in double, y = bf16(w * (float(inv) * x)). */
+void orc_rmsnorm(const uint16_t *x, const uint16_t *w, int rows, int size, uint16_t *out) {
+    double part[256];
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *xr = x + (int64_t)r * size;
+        for (int tid = 0; tid < 256; ++tid) {
+            double ss = 0.0;
+            for (int i = tid; i < size; i += 256) {
+                double v = (double)orc_bf2f(xr[i]);
+                ss += v * v;
+            }
+            part[tid] = ss;
+        }
+        for (int s = 128; s > 0; s >>= 1)
+            for (int tid = 0; tid < s; ++tid) part[tid] += part[tid + s];
+        const double inv = 1.0 / sqrt(part[0] / (double)size + 1e-5);
+        const float invf = (float)inv;
+        for (int i = 0; i < size; ++i) {
+            float v = invf * orc_bf2f(xr[i]);
+            out[(int64_t)r * size + i] = orc_f2bf(orc_bf2f(w[i]) * v);
+        }
+    }
+}
+
+/* accumulate_kernel_bf16 with factor 1 (other_kernels.hpp:17-35). */
+void orc_residual_add(uint16_t *x, const uint16_t *e, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = orc_f2bf(orc_bf2f(x[i]) + orc_bf2f(e[i]) * 1.0f);
+}
+
+/* Whole MoE on normalised rows, getp semantics: router (or forced routing
+ * when ti_in != NULL), experts, reduction.  Optional outputs may be NULL. */
+void orc_moe_forward(int H, int D, int E, int K, float limit, float alpha, const uint16_t *x_norm,
+                     const uint16_t *wr, const uint16_t *br, const uint8_t *w1, const uint8_t *s1,
+                     const uint16_t *b1, const uint8_t *w2, const uint8_t *s2, const uint16_t *b2,
+                     int T, const int32_t *ti_in, const uint16_t *tw_in, uint16_t *e_agg,
+                     uint16_t *logits_out, int32_t *ti_out, uint16_t *tw_out) {
+    int32_t *ti = (int32_t *)malloc(sizeof(int32_t) * (size_t)T * K + 4);
+    uint16_t *tw = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * K + 4);
+    if (ti_in) {
+        memcpy(ti, ti_in, sizeof(int32_t) * (size_t)T * K);
+        memcpy(tw, tw_in, sizeof(uint16_t) * (size_t)T * K);
+    } else {
+        uint16_t *lg = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * E + 2);
+        orc_router_logits(x_norm, wr, T, H, E, lg);
+        orc_topk_softmax(lg, br, T, E, K, ti, tw);
+        if (logits_out) memcpy(logits_out, lg, sizeof(uint16_t) * (size_t)T * E);
+        free(lg);
+    }
+    orc_moe_experts(H, D, E, K, limit, alpha, x_norm, w1, s1, b1, w2, s2, b2, ti, tw, T, e_agg,
+                    NULL);
+    if (ti_out) memcpy(ti_out, ti, sizeof(int32_t) * (size_t)T * K);
+    if (tw_out) memcpy(tw_out, tw, sizeof(uint16_t) * (size_t)T * K);
+    free(ti);
+    free(tw);
+}
+
+/* ------------------------------------------------- fp32 CPU engine ----- */
+
+/* matmul (run.cpp:355-368): OpenMP over output rows, double accumulation of
+ * fp32 products. */
+static void orc_matmul_f32(float *xout, const float *x, const float *w, int n, int d) {
+    int i;
+#pragma omp parallel for private(i)
+    for (i = 0; i < d; i++) {
+        double val = 0.0;
+        for (int j = 0; j < n; j++) val += (double)(w[(int64_t)i * n + j] * x[j]);
+        xout[i] = (float)val;
+    }
+}
+
+typedef struct {
+    float value;
+    int index;
+} orc_pair;
+
+/* topk (run.cpp:387-420) sorts (value, index) pairs descending with qsort;
+ * a stable insertion sort reproduces glibc's (merge-sort) order, ties keeping
+ * ascending index. */
+static void orc_topk_f32(float *vals, int *idx, const float *score, int E, int K) {
+    orc_pair p[256];
+    for (int i = 0; i < E; ++i) {
+        p[i].value = score[i];
+        p[i].index = i;
+        int j = i;
+        while (j > 0 && p[j - 1].value < p[j].value) {
+            orc_pair tmp = p[j - 1];
+            p[j - 1] = p[j];
+            p[j] = tmp;
+            --j;
+        }
+    }
+    for (int i = 0; i < K; ++i) {
+        vals[i] = p[i].value;
+        idx[i] = p[i].index;
+    }
+}
+
+/*
+ * One token through the CPU engine's MoE block (run.cpp:657-748) with fp32
+ * weights (w1f [E][2D][H], w2f [E][H][D]) and fp32 router.  x is the
+ * normalised token row; e_agg (fp32 [H]) is the MoE output.  scratch needs
+ * 2D + 3D + H + E floats.  Experts are visited in ascending index order as in
+ * run.cpp:689-747.
+ */
+void orc_moe_fp32_token(int H, int D, int E, int K, float limit, const float *x, const float *wr,
+                        const float *br, const float *w1f, const float *b1f, const float *w2f,
+                        const float *b2f, float *e_agg, float *scratch) {
+    float *mlp1 = scratch, *gate = mlp1 + 2 * D, *up = gate + D, *gu = up + D;
+    float *tb2 = gu + D, *score = tb2 + H;
+    float topv[8];
+    int topi[8];
+    orc_matmul_f32(score, x, wr, H, E);
+    for (int i = 0; i < E; ++i) score[i] += br[i];
+    orc_topk_f32(topv, topi, score, E, K);
+    /* softmax (run.cpp:335-353) over the K selected */
+    double mx = topv[0];
+    for (int i = 1; i < K; ++i)
+        if (topv[i] > mx) mx = topv[i];
+    double sum = 0.0;
+    for (int i = 0; i < K; ++i) {
+        topv[i] = expf((float)(topv[i] - mx));
+        sum += topv[i];
+    }
+    for (int i = 0; i < K; ++i) topv[i] = (float)(topv[i] / sum);
+    memset(e_agg, 0, sizeof(float) * H);
+    const float alpha = 1.702f;
+    for (int e = 0; e < E; ++e) {
+        float ew = 0.0f;
+        int in = 0;
+        for (int i = 0; i < K; ++i)
+            if (topi[i] == e) {
+                in = 1;
+                ew = topv[i];
+                break;
+            }
+        if (!in) continue;
+        orc_matmul_f32(mlp1, x, w1f + (int64_t)e * 2 * D * H, H, 2 * D);
+        for (int i = 0; i < 2 * D; ++i) mlp1[i] += b1f[(int64_t)e * 2 * D + i];
+        for (int j = 0; j < D; ++j) {
+            gate[j] = mlp1[2 * j];
+            up[j] = mlp1[2 * j + 1];
+        }
+        for (int i = 0; i < D; ++i) {
+            float v = gate[i], u = up[i];
+            if (v > limit) v = limit;
+            if (u > limit) u = limit;
+            if (u < -limit) u = -limit;
+            v *= (1.0f / (1.0f + expf(-alpha * v)));
+            v *= (u + 1.0f);
+            gu[i] = v;
+        }
+        orc_matmul_f32(tb2, gu, w2f + (int64_t)e * H * D, D, H);
+        for (int i = 0; i < H; ++i) tb2[i] += b2f[(int64_t)e * H + i];
+        for (int i = 0; i < H; ++i) e_agg[i] += tb2[i] * ew;
+    }
+}
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

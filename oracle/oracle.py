@@ -1,0 +1,198 @@
+"""ctypes bindings of the CPU oracle (moe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  The product path never uses it.
+bf16 values are uint16 bit patterns; all arrays are C-contiguous numpy.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+_SIGS = {
+    "orc_f2bf": (ctypes.c_uint16, [_F]),
+    "orc_bf2f": (_F, [ctypes.c_uint16]),
+    "orc_dequant_mxfp4": (None, [_P, _P, _I64, _P]),
+    "orc_dequant_mxfp4_f32": (None, [_P, _P, _I64, _P]),
+    "orc_router_logits": (None, [_P, _P, _I, _I, _I, _P]),
+    "orc_topk_softmax": (None, [_P, _P, _I, _I, _I, _P, _P]),
+    "orc_route_index": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "orc_moe_experts": (None, [_I, _I, _I, _I, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                               _P, _P]),
+    "orc_rmsnorm": (None, [_P, _P, _I, _I, _P]),
+    "orc_residual_add": (None, [_P, _P, _I64]),
+    "orc_moe_forward": (None, [_I, _I, _I, _I, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                               _P, _P, _P, _P, _P, _P]),
+    "orc_moe_fp32_token": (None, [_I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "orc_num_threads": (_I, []),
+}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        for n, (r, a) in _SIGS.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def dequant(packed, scales, n: int) -> np.ndarray:
+    packed, scales = _c(packed, np.uint8), _c(scales, np.uint8)
+    out = np.empty(n, np.uint16)
+    lib().orc_dequant_mxfp4(_p(packed), _p(scales), n, _p(out))
+    return out
+
+
+def dequant_f32(packed, scales, n: int) -> np.ndarray:
+    packed, scales = _c(packed, np.uint8), _c(scales, np.uint8)
+    out = np.empty(n, np.float32)
+    lib().orc_dequant_mxfp4_f32(_p(packed), _p(scales), n, _p(out))
+    return out
+
+
+def router_logits(x, wr) -> np.ndarray:
+    x, wr = _c(x, np.uint16), _c(wr, np.uint16)
+    T, H = x.shape
+    E = wr.shape[0]
+    out = np.empty((T, E), np.uint16)
+    lib().orc_router_logits(_p(x), _p(wr), T, H, E, _p(out))
+    return out
+
+
+def topk_softmax(logits, bias, K: int):
+    logits, bias = _c(logits, np.uint16), _c(bias, np.uint16)
+    T, E = logits.shape
+    ti = np.empty((T, K), np.int32)
+    tw = np.empty((T, K), np.uint16)
+    lib().orc_topk_softmax(_p(logits), _p(bias), T, E, K, _p(ti), _p(tw))
+    return ti, tw
+
+
+def route_index(ti, tw, E: int) -> dict:
+    ti, tw = _c(ti, np.int32), _c(tw, np.uint16)
+    T, K = ti.shape
+    counts = np.empty(E, np.int32)
+    offsets = np.empty(E + 1, np.int32)
+    local_ids = np.empty((T, K), np.int32)
+    row_token = np.empty(T * K + 1, np.int32)
+    row_w = np.empty(T * K + 1, np.float32)
+    dropped = lib().orc_route_index(_p(ti), _p(tw), T, K, E, _p(counts), _p(offsets),
+                                    _p(local_ids), _p(row_token), _p(row_w))
+    P = int(offsets[E])
+    return {"counts": counts, "offsets": offsets, "local_ids": local_ids,
+            "row_token": row_token[:P], "row_weight": row_w[:P], "dropped": dropped}
+
+
+def moe_experts(d, x_norm, ti, tw, want_act=False):
+    c = d.cfg
+    x_norm = _c(x_norm, np.uint16)
+    ti, tw = _c(ti, np.int32), _c(tw, np.uint16)
+    T = x_norm.shape[0]
+    out = np.empty((T, c.hidden), np.uint16)
+    act = np.empty((T * c.top_k, c.intermediate), np.uint16) if want_act else None
+    lib().orc_moe_experts(c.hidden, c.intermediate, c.n_experts, c.top_k, 7.0, 1.702,
+                          _p(x_norm), _p(d.w1), _p(d.s1), _p(d.b1), _p(d.w2), _p(d.s2),
+                          _p(d.b2), _p(ti), _p(tw), T, _p(out), _p(act))
+    return (out, act) if want_act else out
+
+
+def moe_forward(d, x_norm=None, forced=True, rows=None):
+    """getp-semantics MoE of a synth.MoeData layer.  Returns dict with
+    e_agg, logits (router runs only), topk_i, topk_w.  `rows` selects a
+    subset of tokens (each token's result depends on that token only)."""
+    c = d.cfg
+    x = d.x if x_norm is None else x_norm
+    fi, fw = (d.forced_i, d.forced_w) if forced else (None, None)
+    if rows is not None:
+        x = x[rows]
+        if fi is not None:
+            fi, fw = fi[rows], fw[rows]
+    x = _c(x, np.uint16)
+    T = x.shape[0]
+    E, K = c.n_experts, c.top_k
+    e_agg = np.empty((T, c.hidden), np.uint16)
+    lg = np.zeros((T, E), np.uint16)
+    ti = np.empty((T, K), np.int32)
+    tw = np.empty((T, K), np.uint16)
+    if fi is not None:
+        fi, fw = _c(fi, np.int32), _c(fw, np.uint16)
+    lib().orc_moe_forward(c.hidden, c.intermediate, E, K, 7.0, 1.702, _p(x), _p(d.router_w),
+                          _p(d.router_b), _p(d.w1), _p(d.s1), _p(d.b1), _p(d.w2), _p(d.s2),
+                          _p(d.b2), T, _p(fi), _p(fw), _p(e_agg), _p(lg), _p(ti), _p(tw))
+    return {"e_agg": e_agg, "logits": lg if fi is None else None, "topk_i": ti, "topk_w": tw}
+
+
+def rmsnorm(x, w) -> np.ndarray:
+    x, w = _c(x, np.uint16), _c(w, np.uint16)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x), _p(w), x.shape[0], x.shape[1], _p(out))
+    return out
+
+
+def residual_add(x, e) -> np.ndarray:
+    x = _c(x, np.uint16).copy()
+    e = _c(e, np.uint16)
+    lib().orc_residual_add(_p(x), _p(e), x.size)
+    return x
+
+
+class Fp32Engine:
+    """The CPU engine's MoE block (run.cpp:657-748) over fp32 weights that are
+    the exact dequantisation of a synth.MoeData layer."""
+
+    def __init__(self, d):
+        from synth import bf16_to_f32  # noqa: E402 (package dir on sys.path)
+        c = d.cfg
+        self.c = c
+        H, D, E = c.hidden, c.intermediate, c.n_experts
+        self.wr = bf16_to_f32(d.router_w).copy()
+        self.br = bf16_to_f32(d.router_b).copy()
+        self.w1 = dequant_f32(d.w1, d.s1, E * 2 * D * H)
+        self.b1 = bf16_to_f32(d.b1).copy()
+        self.w2 = dequant_f32(d.w2, d.s2, E * H * D)
+        self.b2 = bf16_to_f32(d.b2).copy()
+        self.scratch = np.empty(2 * D + 3 * D + H + E + 16, np.float32)
+
+    def token(self, x_row_f32: np.ndarray) -> np.ndarray:
+        c = self.c
+        x = _c(x_row_f32, np.float32)
+        out = np.empty(c.hidden, np.float32)
+        lib().orc_moe_fp32_token(c.hidden, c.intermediate, c.n_experts, c.top_k, 7.0, _p(x),
+                                 _p(self.wr), _p(self.br), _p(self.w1), _p(self.b1), _p(self.w2),
+                                 _p(self.b2), _p(out), _p(self.scratch))
+        return out
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
