@@ -1,0 +1,88 @@
+"""The C ABI library loads, exports every function include/gptoss_moe.h
+declares, and rejects bad arguments with status codes, without a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import gptoss_moe as gm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gptoss_moe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gptoss_moe_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = gm.load_library()
+    names = declared_functions()
+    assert len(names) >= 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python mirror binds every declared entry point
+    assert set(names) <= set(gm._SIGS)
+
+
+def test_version_string():
+    assert gm.load_library().gptoss_moe_version().startswith(b"gptoss_moe")
+
+
+def test_workspace_size():
+    s20 = gm.make_shape(2880, 2880, 32, 4)
+    a = gm.workspace_size(s20, 256)
+    b = gm.workspace_size(s20, 512)
+    assert 0 < a < b
+    # act (P*D bf16) and token-order slots (P*H bf16) dominate
+    P = 256 * 4
+    assert a >= P * 2880 * 2 * 2
+    assert a % 256 == 0
+
+
+@pytest.mark.parametrize("bad", [
+    dict(hidden=2880 + 16), dict(intermediate=100), dict(n_experts=0), dict(n_experts=257),
+    dict(top_k=0), dict(top_k=9), dict(n_experts=2, top_k=3)])
+def test_invalid_shapes_rejected(bad):
+    kw = dict(hidden=2880, intermediate=2880, n_experts=32, top_k=4)
+    kw.update(bad)
+    s = gm.make_shape(**kw)
+    assert gm.workspace_size(s, 16) == 0
+    lib = gm.load_library()
+    w = gm.Weights()
+    rc = lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None, 0,
+                                None, 0, 16, None)
+    assert rc == gm.ERR_INVALID_ARG
+
+
+def test_argument_errors_without_gpu():
+    lib = gm.load_library()
+    s = gm.make_shape(128, 128, 4, 2)
+    w = gm.Weights()
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    # n_tokens > max_tokens
+    assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 9, None, None,
+                                  0, fake, 1 << 30, 8, None) == gm.ERR_INVALID_ARG
+    # only one of forced_i / forced_w
+    assert lib.gptoss_moe_route(ctypes.byref(s), ctypes.byref(w), None, 4, fake, None, fake,
+                                1 << 30, 8, None) == gm.ERR_INVALID_ARG
+    # router pointers missing when not forced
+    assert lib.gptoss_moe_route(ctypes.byref(s), ctypes.byref(w), None, 4, None, None, fake,
+                                1 << 30, 8, None) == gm.ERR_INVALID_ARG
+    # workspace too small
+    w.router_w = w.router_b = 1 << 20
+    assert lib.gptoss_moe_route(ctypes.byref(s), ctypes.byref(w), None, 4, None, None, fake,
+                                64, 8, None) == gm.ERR_WORKSPACE
+    # unknown flag bits
+    need = gm.workspace_size(s, 8)
+    assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
+                                  2, fake, need, 8, None) == gm.ERR_INVALID_ARG
+    # hidden beyond the router's register budget
+    big = gm.make_shape(4096 + 32, 128, 4, 2)
+    assert lib.gptoss_moe_route(ctypes.byref(big), ctypes.byref(w), None, 4, None, None, fake,
+                                1 << 40, 8, None) == gm.ERR_UNSUPPORTED
+    assert lib.gptoss_moe_rmsnorm(None, None, None, 1, 8, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_dequant_mxfp4(None, None, 1, 1, 1, None, None) == gm.ERR_INVALID_ARG
