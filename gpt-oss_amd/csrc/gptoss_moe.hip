@@ -1,9 +1,9 @@
 // gptoss_moe.hip — MI355X (gfx950) MXFP4 mixture-of-experts layer.
 //
 // Kernels (one stream, no host round trip):
-//   route_kernel   router GEMM (pinned fp32 order) + top-k/softmax + expert
-//                  histogram; the last workgroup scans the histogram and
-//                  writes the per-expert tile list.
+//   router_kernel  router GEMM in a pinned fp32 order (bit-reproducible).
+//   topk_kernel    top-k/softmax + expert histogram; the last workgroup
+//                  scans the histogram and writes the per-expert tile list.
 //   index_kernel   per-expert ballot compaction: compact row -> token map.
 //   mlp1_kernel    grouped GEMM x[token(row)] . W1[e]^T, MXFP4 dequantised
 //                  in registers (v_cvt_scalef32_pk_bf16_fp4) into bf16 MFMA
@@ -26,6 +26,7 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;  // register-friendly 16 bytes
 
 constexpr int kWave = 64;
 constexpr int kMaxExperts = 256;
@@ -35,7 +36,6 @@ constexpr int kTileRows = 64;       // rows per grouped-GEMM tile (4 x 16)
 constexpr int kBlockN = 128;        // weight rows per workgroup (4 waves x 32)
 constexpr int kChunkK = 256;        // k per LDS chunk of activations
 constexpr int kUnits = kChunkK / 8; // 16-byte units per LDS row
-constexpr int kPipe = 4;            // k-groups (128 k) of weights in flight
 
 // ----------------------------------------------------------------- bf16 --
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
@@ -69,7 +69,7 @@ __device__ __forceinline__ uint32_t zero_scale_fix(uint32_t q, uint32_t e) {
 // ------------------------------------------------------- workspace map --
 struct WsLayout {
     size_t hdr, counts_hot, counts, offsets, tiles, logits, topk_i, topk_w, local_ids, row_token,
-        row_w, row_slot, act, slots, total;
+        row_w, row_slot, xg, act, slots, total;
     int max_tiles;
 };
 
@@ -103,6 +103,7 @@ WsLayout ws_layout(const gptoss_moe_shape &s, int max_tokens) {
     L.row_token = take(P * 4);
     L.row_w = take(P * 4);
     L.row_slot = take(P * 4);
+    L.xg = take(P * (size_t)s.hidden * 2);
     L.act = take(P * (size_t)s.intermediate * 2);
     L.slots = take(P * (size_t)s.hidden * 2);
     L.total = o;
@@ -124,90 +125,108 @@ __device__ __forceinline__ bool better_pick(float av, int ai, float bv, int bi) 
     return false;
 }
 
-constexpr int kRouteTokens = 2;  // tokens per route workgroup
-
-// One workgroup of 256 threads per kRouteTokens tokens.
-//  - router: wave w computes experts e = w, w+4, ... for the tokens; each
-//    logit is 64 lane-partial fmaf chains over k = 512 i + 8 l + j plus an
-//    xor butterfly, rounded to bf16 (the order the oracle restates);
-//  - top-k: wave tt selects for token tt, reproducing the reference's
-//    halving-tree arg-max over clamp(nextpow2(E), 64, 512) threads
-//    (moe.hpp:465-599) with 64 lanes x R slots;
-//  - histogram via device atomics; the last workgroup to finish scans the
-//    histogram (and resets it) and writes offsets and the tile list.
-__global__ __launch_bounds__(256) void route_kernel(
-    const uint16_t *__restrict__ x, const uint16_t *__restrict__ wr, const uint16_t *__restrict__ br,
-    const int32_t *__restrict__ forced_i, const uint16_t *__restrict__ forced_w, int T, int H, int E,
-    int K, uint16_t *__restrict__ logits, int32_t *__restrict__ topk_i, uint16_t *__restrict__ topk_w,
-    int32_t *__restrict__ local_ids, int32_t *counts_hot, int32_t *__restrict__ counts,
-    int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr, int nthreads_ref) {
-    __shared__ float s_score[kRouteTokens][kMaxExperts];
-    __shared__ int s_last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.x * kRouteTokens;
-
-    if (forced_i == nullptr) {
-        // ---- router logits
-        constexpr int NI = kMaxHidden / 512;
-        float xf[kRouteTokens][NI][8];
-        const int ni = (H + 511) / 512;
+// Router logits: logits[t][e] = bf16(x[t] . wr[e]) in fp32, no bias
+// (matmul_vec128_singlebuf_Abf16, matmul.hpp:1344, called at
+// getp_run.cpp:2612-2620).  The fp32 order is pinned so the CPU oracle can
+// reproduce every logit bit for bit: 16 partial sums p[l] (l = 0..15), each
+// an fmaf chain over k = 128 i + 8 l + j (i ascending, then j = 0..7), then
+// p[l] += p[l ^ s] for s = 8, 4, 2, 1.  A 16-lane group computes TT tokens x
+// EE experts of such dot products (lane l owns partial l of all of them), so
+// each loaded bf16 is converted once and used TT or EE times.
+template <int TT, int EE>
+__global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict__ x,
+                                                    const uint16_t *__restrict__ wr, int T, int H,
+                                                    int E, uint16_t *__restrict__ logits) {
+    const int lane16 = threadIdx.x & 15;
+    const int grp = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int n_eb = (E + EE - 1) / EE;
+    const int eb = grp % n_eb, tb = grp / n_eb;
+    if (tb * TT >= T) return;  // whole 16-lane group idle (no shuffles follow for it)
+    const uint16_t *xp[TT];
+    const uint16_t *wp[EE];
 #pragma unroll
-        for (int tt = 0; tt < kRouteTokens; ++tt) {
-            const int t = min(t0 + tt, T - 1);
+    for (int i = 0; i < TT; ++i) xp[i] = x + (size_t)min(tb * TT + i, T - 1) * H;
 #pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const int k = 512 * i + 8 * lane;
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (i < ni && k < H) v = *reinterpret_cast<const uint4 *>(x + (size_t)t * H + k);
-                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    for (int i = 0; i < EE; ++i) wp[i] = wr + (size_t)min(eb * EE + i, E - 1) * H;
+    float acc[TT][EE];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    xf[tt][i][2 * j] = __uint_as_float(d[j] << 16);
-                    xf[tt][i][2 * j + 1] = __uint_as_float(d[j] & 0xffff0000u);
-                }
-            }
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < EE; ++j) acc[i][j] = 0.f;
+    // NB iterations' loads are issued before any of them is used
+    constexpr int NB = (TT + EE) <= 2 ? 4 : (TT + EE) <= 6 ? 2 : 1;
+    const int NI = (H + 127) / 128;
+    for (int it0 = 0; it0 < NI; it0 += NB) {
+        uint4 xv[NB][TT], wv[NB][EE];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int k = min(128 * (it0 + b) + 8 * lane16, H - 8);
+#pragma unroll
+            for (int i = 0; i < TT; ++i) xv[b][i] = *reinterpret_cast<const uint4 *>(xp[i] + k);
+#pragma unroll
+            for (int i = 0; i < EE; ++i) wv[b][i] = *reinterpret_cast<const uint4 *>(wp[i] + k);
         }
-        for (int e = wave; e < E; e += 4) {
-            float p[kRouteTokens];
 #pragma unroll
-            for (int tt = 0; tt < kRouteTokens; ++tt) p[tt] = 0.f;
-            const uint16_t *wrow = wr + (size_t)e * H;
+        for (int b = 0; b < NB; ++b) {
+            if (128 * (it0 + b) + 8 * lane16 >= H) break;  // no partial of this lane left
 #pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const int k = 512 * i + 8 * lane;
-                if (i < ni && k < H) {
-                    const uint4 v = *reinterpret_cast<const uint4 *>(wrow + k);
-                    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+            for (int q = 0; q < 4; ++q) {
+                float xl[TT], xh[TT];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float w0 = __uint_as_float(d[j] << 16);
-                        const float w1 = __uint_as_float(d[j] & 0xffff0000u);
+                for (int i = 0; i < TT; ++i) {
+                    const uint4 v = xv[b][i];
+                    const uint32_t d = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+                    xl[i] = __uint_as_float(d << 16);
+                    xh[i] = __uint_as_float(d & 0xffff0000u);
+                }
 #pragma unroll
-                        for (int tt = 0; tt < kRouteTokens; ++tt) {
-                            p[tt] = __builtin_fmaf(xf[tt][i][2 * j], w0, p[tt]);
-                            p[tt] = __builtin_fmaf(xf[tt][i][2 * j + 1], w1, p[tt]);
-                        }
+                for (int j = 0; j < EE; ++j) {
+                    const uint4 v = wv[b][j];
+                    const uint32_t d = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+                    const float wl = __uint_as_float(d << 16), wh = __uint_as_float(d & 0xffff0000u);
+#pragma unroll
+                    for (int i = 0; i < TT; ++i) {
+                        acc[i][j] = __builtin_fmaf(xl[i], wl, acc[i][j]);
+                        acc[i][j] = __builtin_fmaf(xh[i], wh, acc[i][j]);
                     }
                 }
             }
-#pragma unroll
-            for (int tt = 0; tt < kRouteTokens; ++tt) {
-                float v = p[tt];
-#pragma unroll
-                for (int s = 32; s >= 1; s >>= 1) v = __fadd_rn(v, __shfl_xor(v, s, 64));
-                const int t = t0 + tt;
-                if (lane == 0 && t < T) {
-                    const uint16_t lb = f2bf(v);
-                    logits[(size_t)t * E + e] = lb;
-                    s_score[tt][e] = __fadd_rn(bf2f(lb), bf2f(br[e]));
-                }
-            }
         }
-        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < EE; ++j) {
+            float v = acc[i][j];
+#pragma unroll
+            for (int st = 8; st >= 1; st >>= 1) v = __fadd_rn(v, __shfl_xor(v, st, 16));
+            const int t = tb * TT + i, e = eb * EE + j;
+            if (lane16 == 0 && t < T && e < E) logits[(size_t)t * E + e] = f2bf(v);
+        }
+}
 
-        // ---- top-k + softmax, one wave per token
-        if (wave < kRouteTokens && t0 + wave < T) {
-            const int t = t0 + wave;
+constexpr int kTopkTokens = 4;  // one wave per token
+
+// Top-k + softmax (route_select_softmax_kernel_bf16io, moe.hpp:465-599) for
+// one token per wave: scores fp32 = logit + bias; K rounds of the reference's
+// arg-max, a halving tree over clamp(nextpow2(E), 64, 512) threads, emulated
+// exactly with 64 lanes x R slots (slot r of lane l = thread l + 64 r); then
+// softmax over the K selected.  Counts live slots per expert with device
+// atomics; the last workgroup to finish scans the histogram (resetting it)
+// into counts, offsets and the tile list.  With forced routing the given
+// indices and weights are copied and validated instead.
+__global__ __launch_bounds__(256) void topk_kernel(
+    const uint16_t *__restrict__ logits, const uint16_t *__restrict__ br,
+    const int32_t *__restrict__ forced_i, const uint16_t *__restrict__ forced_w, int T, int E,
+    int K, int32_t *__restrict__ topk_i, uint16_t *__restrict__ topk_w,
+    int32_t *__restrict__ local_ids, int32_t *counts_hot, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr, int nthreads_ref) {
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.x * kTopkTokens + wave;
+
+    if (forced_i == nullptr) {
+        if (t < T) {
             const int R = nthreads_ref / 64;  // 1, 2 or 4 slots per lane
             float sv[4];
             int si[4];
@@ -216,12 +235,14 @@ __global__ __launch_bounds__(256) void route_kernel(
             for (int r = 0; r < 4; ++r) {
                 const int i = lane + 64 * r;
                 const bool ok = r < R && i < E;
-                sv[r] = ok ? s_score[wave][i] : -INFINITY;
+                sv[r] = ok ? __fadd_rn(bf2f(logits[(size_t)t * E + i]), bf2f(br[i])) : -INFINITY;
                 si[r] = ok ? i : E;
             }
             int sel_i[kMaxTopK];
             float sel_v[kMaxTopK];
-            for (int s = 0; s < K; ++s) {
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; ++s) {
+                if (s >= K) break;
                 float cv[4];
                 int ci[4];
 #pragma unroll
@@ -230,16 +251,21 @@ __global__ __launch_bounds__(256) void route_kernel(
                     cv[r] = live ? sv[r] : -INFINITY;
                     ci[r] = live ? si[r] : E;
                 }
-                // tree strides >= 64 of the reference: combine slots
-                for (int q = R >> 1; q >= 1; q >>= 1)
-                    for (int r = 0; r < q; ++r)
-                        if (better_pick(cv[r + q], ci[r + q], cv[r], ci[r])) {
-                            cv[r] = cv[r + q];
-                            ci[r] = ci[r + q];
-                        }
+                // tree strides >= 64 of the reference: combine slots r and r + q
+                auto comb = [&](int r, int q) {
+                    if (better_pick(cv[r + q], ci[r + q], cv[r], ci[r])) {
+                        cv[r] = cv[r + q];
+                        ci[r] = ci[r + q];
+                    }
+                };
+                if (R == 4) {
+                    comb(0, 2);
+                    comb(1, 2);
+                }
+                if (R >= 2) comb(0, 1);
                 float bv = cv[0];
                 int bi = ci[0];
-                // tree strides 32..1: lanes l < s take lane l+s's pick if better
+                // tree strides 32..1: lane l < st takes lane l+st's pick if better
 #pragma unroll
                 for (int st = 32; st >= 1; st >>= 1) {
                     const float ov = __shfl_down(bv, st, 64);
@@ -257,14 +283,19 @@ __global__ __launch_bounds__(256) void route_kernel(
             }
             if (lane == 0) {
                 float mx = sel_v[0];
-                for (int s = 1; s < K; ++s) mx = fmaxf(mx, sel_v[s]);
+#pragma unroll
+                for (int s = 1; s < kMaxTopK; ++s)
+                    if (s < K) mx = fmaxf(mx, sel_v[s]);
                 float ex[kMaxTopK], sum = 0.f;
-                for (int s = 0; s < K; ++s) {
-                    ex[s] = expf(__fsub_rn(sel_v[s], mx));
-                    sum = __fadd_rn(sum, ex[s]);
+#pragma unroll
+                for (int s = 0; s < kMaxTopK; ++s) {
+                    ex[s] = s < K ? expf(__fsub_rn(sel_v[s], mx)) : 0.f;
+                    if (s < K) sum = __fadd_rn(sum, ex[s]);
                 }
                 const float inv = 1.f / __fadd_rn(sum, 1e-20f);
-                for (int s = 0; s < K; ++s) {
+#pragma unroll
+                for (int s = 0; s < kMaxTopK; ++s) {
+                    if (s >= K) break;
                     const int e = sel_i[s] < E ? sel_i[s] : -1;
                     topk_i[(size_t)t * K + s] = e;
                     topk_w[(size_t)t * K + s] = f2bf(__fmul_rn(ex[s], inv));
@@ -278,20 +309,19 @@ __global__ __launch_bounds__(256) void route_kernel(
             }
         }
     } else {
-        // ---- forced routing: copy, validate, count
-        if (tid < kRouteTokens * K) {
-            const int tt = tid / K, s = tid % K, t = t0 + tt;
-            if (t < T) {
-                const int e = forced_i[(size_t)t * K + s];
+        if (tid < kTopkTokens * K) {
+            const int tt = blockIdx.x * kTopkTokens + tid / K, s = tid % K;
+            if (tt < T) {
+                const int e = forced_i[(size_t)tt * K + s];
                 bool live = e >= 0 && e < E;
                 for (int j = 0; j < s; ++j)
-                    if (forced_i[(size_t)t * K + j] == e) live = false;
-                topk_i[(size_t)t * K + s] = e;
-                topk_w[(size_t)t * K + s] = forced_w[(size_t)t * K + s];
+                    if (forced_i[(size_t)tt * K + j] == e) live = false;
+                topk_i[(size_t)tt * K + s] = e;
+                topk_w[(size_t)tt * K + s] = forced_w[(size_t)tt * K + s];
                 if (live) {
                     atomicAdd(&counts_hot[e], 1);
                 } else {
-                    local_ids[(size_t)t * K + s] = -1;
+                    local_ids[(size_t)tt * K + s] = -1;
                     atomicAdd(&hdr[HDR_STATUS_HOT], 1);
                 }
             }
@@ -352,16 +382,18 @@ __global__ __launch_bounds__(256) void route_kernel(
     }
 }
 
-// Compact row map (route_build_index_kernel_bf16wts, moe.hpp:1173-1270):
-// one workgroup per expert; rows of expert e are assigned in ascending
-// token order with wave ballots.
+// Compact row map (route_build_index_kernel_bf16wts, moe.hpp:1173-1270): one
+// workgroup per expert; rows of expert e are assigned in ascending token
+// order with wave ballots.
 __global__ __launch_bounds__(256) void index_kernel(const int32_t *__restrict__ topk_i,
                                                    const uint16_t *__restrict__ topk_w, int T, int K,
-                                                   int E, const int32_t *__restrict__ offsets,
+                                                   int E, int H, const int32_t *__restrict__ offsets,
+                                                   const uint16_t *__restrict__ x,
                                                    int32_t *__restrict__ local_ids,
                                                    int32_t *__restrict__ row_token,
                                                    float *__restrict__ row_w,
-                                                   int32_t *__restrict__ row_slot) {
+                                                   int32_t *__restrict__ row_slot,
+                                                   uint16_t *__restrict__ xg) {
     __shared__ int s_wcount[4];
     const int e = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -374,9 +406,7 @@ __global__ __launch_bounds__(256) void index_kernel(const int32_t *__restrict__ 
             for (int s = 0; s < K; ++s) {
                 const int v = topk_i[(size_t)t * K + s];
                 if (v == e) {
-                    bool dup = false;
-                    for (int j = 0; j < s; ++j) dup |= topk_i[(size_t)t * K + j] == e;
-                    if (!dup) kk = s;
+                    kk = s;
                     break;
                 }
             }
@@ -392,7 +422,8 @@ __global__ __launch_bounds__(256) void index_kernel(const int32_t *__restrict__ 
             total += s_wcount[w];
         }
         if (kk >= 0) {
-            const int row = base_row + carry + wbase + rank;
+            const int local = wbase + rank;
+            const int row = base_row + carry + local;
             local_ids[(size_t)t * K + kk] = row;
             row_token[row] = t;
             row_w[row] = bf2f(topk_w[(size_t)t * K + kk]);
@@ -403,23 +434,46 @@ __global__ __launch_bounds__(256) void index_kernel(const int32_t *__restrict__ 
     }
 }
 
+// Gather (pack_rows_kernel_bf16_in, moe.hpp:983-1048): xg[row] = x[token(row)]
+// for the compact rows; workgroups stride over rows, 16 bytes per thread.
+__global__ __launch_bounds__(256) void gather_kernel(const uint16_t *__restrict__ x,
+                                                    const int32_t *__restrict__ row_token,
+                                                    const int32_t *__restrict__ offsets, int E,
+                                                    int H, uint16_t *__restrict__ xg) {
+    const int P = offsets[E];
+    const int h8 = H / 8;
+    const size_t n = (size_t)P * h8;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const int r = (int)(i / h8), c = (int)(i - (size_t)r * h8);
+        *reinterpret_cast<uint4 *>(xg + (size_t)r * H + 8 * c) =
+            *reinterpret_cast<const uint4 *>(x + (size_t)row_token[r] * H + 8 * c);
+    }
+}
+
 // ---------------------------------------------------- grouped GEMM core --
 //
-// Workgroup = 4 waves; a tile of up to 64 activation rows against 128 weight
-// rows (32 per wave).  Weights go HBM -> registers (16 B per lane = one
-// 32-element e8m0 block of one weight row) with kPipe k-groups in flight and
-// are dequantised in registers straight into the bf16 MFMA B operand.
-// Activation rows are staged through LDS in chunks of 256 k with an XOR
-// swizzle (16-byte unit c of row r stored at unit c ^ (r & 15)).
+// One workgroup of 8 waves per CU, persistent over (tile, 128-weight-row
+// block) items; a tile is up to 64 activation rows of one expert.  K is swept
+// in stages of 256 k and the stream of stages runs across the workgroup's
+// items without draining.  The waves specialise, so that each kind of load
+// waits only on its own kind (a wave's loads retire in order):
+//   waves 4, 5  weight producers: full 128-byte row chunks per load
+//               instruction (the pattern that streams HBM at full rate),
+//               kWDepth stages in flight in registers, written to LDS;
+//   waves 6, 7  activation loaders: the stage's 64 x 256 activation chunk
+//               from the compact (gathered) rows, one stage ahead;
+//   waves 0..3  consumers: LDS only -> dequantise (v_cvt_scalef32_pk_bf16_fp4)
+//               -> v_mfma_f32_16x16x32_bf16 -> epilogue.
+// Iteration s: loaders write stage s to LDS slot s & 1 while consumers compute
+// stage s - 1 from slot (s - 1) & 1; one barrier ends the iteration.
 //
-// MFMA v_mfma_f32_16x16x32_bf16: lane l = (n = l & 15, g = l >> 4).  For
-// k-group kg (128 k) the lane's weight bytes cover k = 128 kg + 32 g .. +31;
-// MFMA step s (0..3) takes k = 128 kg + 32 g + 8 s + (0..7) from both the A
-// rows (LDS) and the weight row, which is a permutation of k shared by both
-// operands.  Output: lane holds C[m = 4 g + v][n] for v = 0..3.
+// Consumer wave w owns weight rows 32 w .. 32 w + 31 as two MFMA column tiles.
+// Lane l = (n = l & 15, g = l >> 4): step s = 4 h + q of a stage takes
+// k = 256 j + 32 (g + 4 h) + 8 q + (0..7) from both operands (a permutation of
+// k shared by A and B).  Output: lane holds C[m = 4 g + v][n], v = 0..3.
 
 struct GemmArgs {
-    const uint16_t *A;          // activations (x for MLP1, act for MLP2)
+    const uint16_t *A;          // activation rows in compact order (gathered x for MLP1, act for MLP2)
     const int32_t *row_token;   // compact row -> token
     const int32_t *row_slot;    // compact row -> token-order slot t*k + j
     const uint8_t *Wq;          // MXFP4 nibbles, all experts
@@ -433,207 +487,354 @@ struct GemmArgs {
     float limit, alpha;
 };
 
-// Weight row of tile t (0/1) for this lane: MLP1 pairs gate (t = 0) and up
-// (t = 1) rows of the same output column in the same lane; MLP2 is plain.
+constexpr int kStageK = 256;     // k per stage (128 B of each weight row)
+constexpr int kAUnits = kTileRows * kUnits;  // 16-byte activation units per stage
+
+struct StageSlot {
+    uint8_t w[4][32 * 128];      // [producer/consumer wave][32 rows x 128 B], swizzled
+    uint8_t s[4][32 * 8];        // scales [wave][row][chunk]
+    uint4 a[kAUnits];            // activations [row][unit ^ (row & 15)]
+};
+
+// LDS row (0..31) of the wave's weight row wr (0..31): MLP1 puts gate rows
+// (even) in 0..15 and up rows (odd) in 16..31, so MFMA tile 0 / 1 lane n holds
+// gate / up of output column j = n; MLP2 keeps the order.
 template <bool kMlp1>
-__device__ __forceinline__ int weight_row(int wcol0, int n, int t) {
-    return kMlp1 ? wcol0 + 2 * n + t : wcol0 + 16 * t + n;
+__device__ __forceinline__ int lds_row_of(int wr) {
+    return kMlp1 ? ((wr & 1) << 4) | (wr >> 1) : wr;
 }
 
-template <int MT, bool kMlp1>
-__device__ __forceinline__ void gemm_tile(const GemmArgs &a, const Tile &tl, int nb,
-                                          uint4 *__restrict__ lds) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n_l = lane & 15, g = lane >> 4;
-    const int N = a.N, K = a.K;
-    const int e = tl.expert;
-    const int wcol0 = nb * kBlockN + wave * 32;
-    const bool wave_active = wcol0 < N;  // N is a multiple of 32
-    const int KG = (K + 127) / 128;
-    const int NCH = (K + kChunkK - 1) / kChunkK;
-
-    // ---- weight stream setup
-    const size_t seg_el = (size_t)N * K;
-    const uint8_t *wq = a.Wq + (size_t)e * (seg_el / 2);
-    const uint8_t *ws = a.Ws + (size_t)e * (seg_el / 32);
-    const uint8_t *qptr[2];
-    const uint8_t *sptr[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int row = wave_active ? weight_row<kMlp1>(wcol0, n_l, t) : 0;
-        qptr[t] = wq + ((size_t)row * K + 32 * g) / 2;
-        sptr[t] = ws + ((size_t)row * K + 32 * g) / 32;
+// Work items are (tile, 128-row weight block).  Workgroups are dispatched to
+// the 8 XCDs round robin (workgroup b runs on XCD b % 8), so tile t is given
+// only to XCD t % 8: its activation rows are then re-read by all of its
+// weight blocks from that XCD's L2 instead of being fetched by every XCD.
+// Within an XCD, its Gx workgroups stride over its items.
+struct ItemMap {
+    int nblk, xcd, w, Gx;
+    __device__ __forceinline__ void init(int ntiles, int nblk_, int &n_items) {
+        nblk = nblk_;
+        xcd = (int)blockIdx.x & 7;
+        w = (int)blockIdx.x >> 3;
+        Gx = (int)gridDim.x >> 3;
+        const int tiles_x = ntiles > xcd ? (ntiles - xcd + 7) / 8 : 0;
+        const int items_x = tiles_x * nblk;
+        n_items = items_x > w ? (items_x - w + Gx - 1) / Gx : 0;
     }
-    uint4 q[kPipe][2];
-    uint32_t sc[kPipe][2];
-    auto load_group = [&](int kg, int stage) {
-        const bool ok = wave_active && (kg * 128 + 32 * g < K);
+    __device__ __forceinline__ void at(const Tile *tiles, int i, Tile &tl, int &nb) const {
+        const int ii = w + i * Gx;
+        tl = tiles[xcd + 8 * (ii / nblk)];
+        nb = ii % nblk;
+    }
+};
+
+// Step st of this workgroup's stream -> item tile, weight block and stage.
+__device__ __forceinline__ void step_at(const GemmArgs &a, const ItemMap &im, int NST, int st,
+                                        Tile &tl, int &nb, int &j) {
+    const int i = st / NST;
+    j = st - i * NST;
+    im.at(a.tiles, i, tl, nb);
+}
+
+// Weight producer (waves 4, 5): rows 64 p .. 64 p + 63 of the block, 8 load
+// instructions of 8 rows x one full 128-byte row chunk per stage (lane l: row
+// 8 t + (l >> 3), chunk l & 7), plus the stage's 8 e8m0 bytes of row l as
+// four 2-byte loads (a row's scales are K / 32 bytes apart, so 2-byte
+// aligned).  12 load instructions per stage keep kWDepth stages within the
+// 63 outstanding loads a wave can track.  Invalid lanes write zeros.
+constexpr int kWDepth = 4;
+template <bool kMlp1>
+__device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slots, int total,
+                                               int total_p, const ItemMap &im, int NST) {
+    const int p = (threadIdx.x >> 6) - 4, lane = threadIdx.x & 63;
+    const int rr = lane >> 3, ch = lane & 7;
+    const int N = a.N, K = a.K;
+    uint4 q[kWDepth][8];
+    uint32_t sc[kWDepth][4];  // bytes 2 m, 2 m + 1 of row `lane`'s stage scales
+    int stage_of[kWDepth];
+    bool wval_of[kWDepth][2];
+
+    auto issue = [&](int st, int r) {
+        st = min(st, total - 1);
+        Tile tl;
+        int nb, j;
+        step_at(a, im, NST, st, tl, nb, j);
+        const size_t seg_el = (size_t)N * K;
+        const uint8_t *wq = a.Wq + (size_t)tl.expert * (seg_el / 2);
+        const uint8_t *ws = a.Ws + (size_t)tl.expert * (seg_el / 32);
+        const uint32_t k = (uint32_t)min(j * kStageK + 32 * ch, K - 32);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (ok) {
-                q[stage][t] = *reinterpret_cast<const uint4 *>(qptr[t] + kg * 64);
-                sc[stage][t] = sptr[t][kg * 4];
-            } else {
-                q[stage][t] = make_uint4(0, 0, 0, 0);
-                sc[stage][t] = 0;
+        for (int hh = 0; hh < 2; ++hh) {  // consumer region 2 p + hh
+            const int row0 = nb * kBlockN + (2 * p + hh) * 32;
+            const bool wvalid = row0 < N;
+            wval_of[r][hh] = wvalid;
+            const uint32_t el0 = (uint32_t)(wvalid ? row0 + rr : 0) * (uint32_t)K + k;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t el = el0 + t * 8u * (uint32_t)K;
+                q[r][4 * hh + t] = *reinterpret_cast<const uint4 *>(wq + el / 2);
             }
         }
+        // scales: lane = row (64 p + lane) of the block, bytes 8 j .. 8 j + 7 of
+        // its K / 32 scale bytes; each 2-byte load is clamped inside the row
+        // (K / 32 is even, so every load is 2-byte aligned)
+        const int srow = min(nb * kBlockN + 64 * p + lane, N - 1);
+        const uint32_t sb = (uint32_t)srow * (uint32_t)(K / 32);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            sc[r][m] = *reinterpret_cast<const uint16_t *>(
+                ws + sb + (uint32_t)min(j * 8 + 2 * m, K / 32 - 2));
+        stage_of[r] = j;
+    };
+    // Masks instead of selects: a select on loaded data becomes a branch with
+    // register copies, and the copies would wait for every load in flight.
+    auto write = [&](int r, StageSlot &sl) {
+        const bool kin = stage_of[r] * kStageK + 32 * ch < K;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const uint32_t km = -(uint32_t)(wval_of[r][hh] && kin);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int lr = lds_row_of<kMlp1>(8 * t + rr);
+                const uint4 v = q[r][4 * hh + t];
+                *reinterpret_cast<uint4 *>(&sl.w[2 * p + hh][lr * 128 + 16 * (ch ^ (lr & 7))]) =
+                    make_uint4(v.x & km, v.y & km, v.z & km, v.w & km);
+            }
+        }
+        // scale bytes of row `lane` (region 2 p + lane / 32, row lane % 32), chunks
+        // past K zeroed; rows past N are never read by a live output column
+        const int wr = lane & 31;
+        const int lr = lds_row_of<kMlp1>(wr);
+        const int kc = (K - stage_of[r] * kStageK) / 32;  // live chunks in this stage
+        uint32_t lo = sc[r][0] | (sc[r][1] << 16), hi = sc[r][2] | (sc[r][3] << 16);
+        const uint64_t keep = kc >= 8 ? ~0ull : ((1ull << (8 * kc)) - 1ull);
+        const uint64_t v64 = (((uint64_t)hi << 32) | lo) & keep;
+        *reinterpret_cast<uint64_t *>(&sl.s[2 * p + (lane >> 5)][lr * 8]) = v64;
     };
 
-    // ---- activation staging: thread owns units u = tid + 256 i
-    constexpr int UPT = MT * 16 * kUnits / 256;  // units per thread (2 MT)
-    const uint16_t *arow[UPT];
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-        const int r = (tid + 256 * i) / kUnits;
-        if (r < tl.rows) {
-            const int grow = tl.row0 + r;
-            const size_t src_row = kMlp1 ? (size_t)a.row_token[grow] : (size_t)grow;
-            arow[i] = a.A + src_row * K;
-        } else {
-            arow[i] = nullptr;
+    for (int r = 0; r < kWDepth; ++r) {
+        issue(r, r);  // in slot order: the loop's waits count on it
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int s0 = 0; s0 < total_p; s0 += kWDepth) {
+#pragma unroll
+        for (int r = 0; r < kWDepth; ++r) {
+            // keep each step's use of its loads from being hoisted above the
+            // previous barrier (it would wait for every load in flight)
+            __builtin_amdgcn_sched_barrier(0);
+            write(r, slots[(s0 + r) & 1]);
+            issue(s0 + r + kWDepth, r);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
         }
     }
-    uint4 stage_a[UPT];
-    auto load_a = [&](int ch) {
-#pragma unroll
-        for (int i = 0; i < UPT; ++i) {
-            const int c = (tid + 256 * i) % kUnits;
-            const int k = ch * kChunkK + 8 * c;
-            stage_a[i] = (arow[i] != nullptr && k < K)
-                             ? *reinterpret_cast<const uint4 *>(arow[i] + k)
-                             : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_a = [&]() {
-#pragma unroll
-        for (int i = 0; i < UPT; ++i) {
-            const int u = tid + 256 * i;
-            const int r = u / kUnits, c = u % kUnits;
-            lds[r * kUnits + (c ^ (r & 15))] = stage_a[i];
-        }
-    };
+    __syncthreads();  // iteration total_p: consumers finish the last step
+}
 
+// Activation loader (waves 6, 7): rows 32 p' .. 32 p' + 31 of the 64-row
+// activation chunk (lane l, unit i: row 2 i + (l >> 5), 16-byte unit l & 31,
+// two full 512-byte row chunks per instruction), one stage ahead.  Rows past
+// the tile repeat its last row and k past K repeats the last unit: finite
+// values that meet zero weights or discarded output rows.
+__device__ __forceinline__ void aload_stage(const GemmArgs &a, const ItemMap &im, int NST,
+                                            int total, int st, int p, int lane, u32x4 (&v)[16]) {
+    st = min(st, total - 1);
+#if defined(GPTOSS_DIAG) && GPTOSS_DIAG == 1
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = u32x4{(uint32_t)st, 1u, 2u, 3u};
+    return;
+#endif
+    Tile tl;
+    int nb, j;
+    step_at(a, im, NST, st, tl, nb, j);
+    const int K = a.K;
+    const int k = min(j * kStageK + 8 * (lane & 31), K - 8);
+    const uint16_t *base = a.A + (size_t)tl.row0 * K + k;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int row = min(32 * p + 2 * i + (lane >> 5), tl.rows - 1);
+        v[i] = *reinterpret_cast<const u32x4 *>(base + (uint32_t)row * (uint32_t)K);
+    }
+}
+
+__device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots, int total,
+                                             int total_p, const ItemMap &im, int NST) {
+    const int p = (threadIdx.x >> 6) - 6, lane = threadIdx.x & 63;
+    const int c = lane & 31;
+    u32x4 v[16];
+    aload_stage(a, im, NST, total, 0, p, lane, v);
+    for (int s = 0; s < total_p; ++s) {
+        __builtin_amdgcn_sched_barrier(0);
+        StageSlot &sl = slots[s & 1];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = 32 * p + 2 * i + (lane >> 5);
+            *reinterpret_cast<u32x4 *>(&sl.a[row * kUnits + (c ^ (row & 15))]) = v[i];
+        }
+        aload_stage(a, im, NST, total, s + 1, p, lane, v);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    }
+    __syncthreads();
+}
+
+// One item on a consumer wave: NST stages (one barrier each) then the
+// epilogue.  MT (row tiles of 16) is a template parameter so the
+// accumulators are plain registers with no guarded MFMAs (a guard around an
+// MFMA makes the compiler copy its accumulator in and out).
+template <int MT, bool kMlp1>
+__device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot *slots, int &s,
+                                             const Tile &tl, int nb, int NST) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n_l = lane & 15, g = lane >> 4;
+    const int N = a.N;
     f32x4 acc[MT][2];
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // ---- prologue
-    load_a(0);
-#pragma unroll
-    for (int u = 0; u < kPipe; ++u)
-        if (u < KG) load_group(u, u);
-    store_a();
-    __syncthreads();
-    if (NCH > 1) load_a(1);
-
-    // ---- main loop over k-groups, kPipe at a time so stages are static
-    for (int kg0 = 0; kg0 < KG; kg0 += kPipe) {
-#pragma unroll
-        for (int u = 0; u < kPipe; ++u) {
-            const int kg = kg0 + u;
-            if (kg < KG) {
-                const int cbase = (kg & 1) * 16 + 4 * g;  // LDS unit of step 0
-                if (wave_active) {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        const uint32_t d0 = (s == 0)   ? q[u][0].x
-                                            : (s == 1) ? q[u][0].y
-                                            : (s == 2) ? q[u][0].z
-                                                       : q[u][0].w;
-                        const uint32_t d1 = (s == 0)   ? q[u][1].x
-                                            : (s == 1) ? q[u][1].y
-                                            : (s == 2) ? q[u][1].z
-                                                       : q[u][1].w;
-                        const bf16x8 b0 = dequant8(zero_scale_fix(d0, sc[u][0]), e8m0_to_f32(sc[u][0]));
-                        const bf16x8 b1 = dequant8(zero_scale_fix(d1, sc[u][1]), e8m0_to_f32(sc[u][1]));
-#pragma unroll
-                        for (int m = 0; m < MT; ++m) {
-                            const int r = m * 16 + n_l;
-                            const uint4 av = lds[r * kUnits + ((cbase + s) ^ n_l)];
-                            const bf16x8 af = __builtin_bit_cast(bf16x8, av);
-                            acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b0, acc[m][0], 0, 0, 0);
-                            acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b1, acc[m][1], 0, 0, 0);
-                        }
-                    }
-                }
-                if (kg + kPipe < KG) load_group(kg + kPipe, u);
-                // end of an activation chunk: swap in the next one
-                if ((kg & 1) == 1 && kg + 1 < KG) {
-                    const int next = (kg >> 1) + 1;
-                    __syncthreads();
-                    store_a();
-                    __syncthreads();
-                    if (next + 1 < NCH) load_a(next + 1);
-                }
-            }
+    for (int m = 0; m < MT; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NST; ++j, ++s) {
+        const StageSlot &sl = slots[s & 1];
+        const uint8_t *wb = sl.w[wave];
+        const uint8_t *sb = sl.s[wave];
+#if defined(GPTOSS_DIAG) && GPTOSS_DIAG == 2
+        {
+            const uint4 v = sl.a[lane * 16];
+            const uint4 w = *reinterpret_cast<const uint4 *>(wb + 16 * lane);
+            acc[0][0][0] += __uint_as_float((v.x ^ w.y ^ sb[lane]) & 0x3fffffffu);
         }
-    }
+        if (0)
+#endif
 
-    // ---- epilogues
-    if (!wave_active) return;
-    if (kMlp1) {
-        const int D = N / 2;
-        const int j = wcol0 / 2 + n_l;
-        const float bg = bf2f(a.bias[(size_t)e * N + 2 * j]);
-        const float bu = bf2f(a.bias[(size_t)e * N + 2 * j + 1]);
+        {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int h = 0; h < 2; ++h) {
+            uint4 wv[2];
+            uint32_t se[2];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = m * 16 + 4 * g + v;
-                if (r < tl.rows) {
-                    float gt = bf16_round(acc[m][0][v] + bg);
-                    float up = bf16_round(acc[m][1][v] + bu);
-                    gt = fminf(fmaxf(gt, -a.limit), a.limit);
-                    up = fminf(fmaxf(up, -a.limit), a.limit);
-                    const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
-                    gt = gt * sig;
-                    a.out_act[(size_t)(tl.row0 + r) * D + j] = f2bf(__builtin_fmaf(gt, up, gt));
+            for (int tt = 0; tt < 2; ++tt) {
+                const int lr = 16 * tt + n_l, c = g + 4 * h;
+                wv[tt] = *reinterpret_cast<const uint4 *>(wb + lr * 128 + 16 * (c ^ (lr & 7)));
+                se[tt] = sb[lr * 8 + c];
+                if (se[tt] == 0) {  // e8m0 = 0 -> +-0 (code * 0.0 in the reference); rare
+                    wv[tt].x &= 0x88888888u;
+                    wv[tt].y &= 0x88888888u;
+                    wv[tt].z &= 0x88888888u;
+                    wv[tt].w &= 0x88888888u;
                 }
             }
-    } else {
-        const int H = N;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int h = wcol0 + 16 * t + n_l;
-            const float bb = bf2f(a.bias[(size_t)e * N + h]);
+            uint4 av[MT][4];
 #pragma unroll
             for (int m = 0; m < MT; ++m)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int r = m * 16 + 4 * g + v;
-                    if (r < tl.rows) {
-                        const int row = tl.row0 + r;
-                        a.out_slots[(size_t)a.row_slot[row] * H + h] = f2bf(acc[m][t][v] + bb);
-                    }
+                for (int qd = 0; qd < 4; ++qd)
+                    av[m][qd] = sl.a[(m * 16 + n_l) * kUnits + ((4 * g + 16 * h + qd) ^ n_l)];
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                bf16x8 b[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const uint4 v = wv[tt];
+                    const uint32_t dw = qd == 0 ? v.x : qd == 1 ? v.y : qd == 2 ? v.z : v.w;
+                    b[tt] = dequant8(dw, e8m0_to_f32(se[tt]));
                 }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const bf16x8 af = __builtin_bit_cast(bf16x8, av[m][qd]);
+                    acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[0], acc[m][0], 0, 0, 0);
+                    acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[1], acc[m][1], 0, 0, 0);
+                }
+            }
         }
+        }
+        if (j == NST - 1) {
+            // ---- epilogue of the item
+            const int wcol0 = nb * kBlockN + wave * 32;
+            const int e = tl.expert;
+            if (wcol0 < N) {
+                if (kMlp1) {
+                    const int D = N / 2;
+                    const int jc = wcol0 / 2 + n_l;
+                    const float bg = bf2f(a.bias[(size_t)e * N + 2 * jc]);
+                    const float bu = bf2f(a.bias[(size_t)e * N + 2 * jc + 1]);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int r = m * 16 + 4 * g + v;
+                            if (r < tl.rows) {
+                                float gt = bf16_round(acc[m][0][v] + bg);
+                                float up = bf16_round(acc[m][1][v] + bu);
+                                gt = fminf(fmaxf(gt, -a.limit), a.limit);
+                                up = fminf(fmaxf(up, -a.limit), a.limit);
+                                const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
+                                gt = gt * sig;
+                                a.out_act[(size_t)(tl.row0 + r) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                            }
+                        }
+                } else {
+                    const int H = N;
+                    int slot[MT][4];  // token-order slot of each of this lane's rows
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v)
+                            slot[m][v] = a.row_slot[tl.row0 + min(m * 16 + 4 * g + v, tl.rows - 1)];
+                    float bb[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) bb[t] = bf2f(a.bias[(size_t)e * N + wcol0 + 16 * t + n_l]);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            if (m * 16 + 4 * g + v < tl.rows) {
+                                uint16_t *dst = a.out_slots + (size_t)slot[m][v] * H + wcol0 + n_l;
+                                dst[0] = f2bf(acc[m][0][v] + bb[0]);
+                                dst[16] = f2bf(acc[m][1][v] + bb[1]);
+                            }
+                        }
+                }
+            }
+        }
+        __syncthreads();
     }
 }
 
-// Persistent grouped GEMM: workgroups stride over (tile, 128-row weight block)
-// items; the tile count comes from the device-side tile list.
 template <bool kMlp1>
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
-    __shared__ uint4 lds[kTileRows * kUnits];
-    const int ntiles = a.hdr[HDR_NTILES];
-    const int nblk = (a.N + kBlockN - 1) / kBlockN;
-    const int items = ntiles * nblk;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
-        const Tile tl = a.tiles[it / nblk];
-        const int nb = it % nblk;
-        const int mt = (tl.rows + 15) / 16;
-        __syncthreads();  // previous item finished with LDS
-        switch (mt) {
-            case 1: gemm_tile<1, kMlp1>(a, tl, nb, lds); break;
-            case 2: gemm_tile<2, kMlp1>(a, tl, nb, lds); break;
-            case 3: gemm_tile<3, kMlp1>(a, tl, nb, lds); break;
-            default: gemm_tile<4, kMlp1>(a, tl, nb, lds); break;
+__device__ __forceinline__ void gemm_consumer(const GemmArgs &a, StageSlot *slots, int n_items,
+                                              int total_p, const ItemMap &im, int NST) {
+    __syncthreads();  // iteration 0: producers fill stage 0
+    int s = 0;
+    for (int i = 0; i < n_items; ++i) {
+        Tile tl;
+        int nb;
+        im.at(a.tiles, i, tl, nb);
+        switch ((tl.rows + 15) / 16) {
+            case 1: consume_item<1, kMlp1>(a, slots, s, tl, nb, NST); break;
+            case 2: consume_item<2, kMlp1>(a, slots, s, tl, nb, NST); break;
+            case 3: consume_item<3, kMlp1>(a, slots, s, tl, nb, NST); break;
+            default: consume_item<4, kMlp1>(a, slots, s, tl, nb, NST); break;
         }
     }
+    for (; s < total_p; ++s) __syncthreads();  // producers' padding steps
+}
+
+template <bool kMlp1>
+__global__ __launch_bounds__(512) void grouped_gemm_kernel(GemmArgs a) {
+    __shared__ StageSlot slots[2];
+    const int ntiles = a.hdr[HDR_NTILES];
+    ItemMap im;
+    int n_items;
+    im.init(ntiles, (a.N + kBlockN - 1) / kBlockN, n_items);
+    const int NST = (a.K + kStageK - 1) / kStageK;
+    if (n_items == 0) return;
+    const int total = n_items * NST;
+    const int total_p = (total + kWDepth - 1) / kWDepth * kWDepth;
+    const int wave = threadIdx.x >> 6;
+    if (wave < 4)
+        gemm_consumer<kMlp1>(a, slots, n_items, total_p, im, NST);
+    else if (wave < 6)
+        gemm_wproducer<kMlp1>(a, slots, total, total_p, im, NST);
+    else
+        gemm_aloader(a, slots, total, total_p, im, NST);
 }
 
 // Weighted top-k reduction (reduce_tokenwise_expert_outputs_bf16_bf16wts,
@@ -769,7 +970,7 @@ int device_cus() {
 bool shape_ok(const gptoss_moe_shape *s) {
     if (!s) return false;
     if (s->hidden <= 0 || s->intermediate <= 0) return false;
-    if (s->hidden % 32 || s->intermediate % 32) return false;
+    if (s->hidden % 64 || s->intermediate % 64) return false;
     if (s->n_experts < 1 || s->n_experts > kMaxExperts) return false;
     if (s->top_k < 1 || s->top_k > kMaxTopK || s->top_k > s->n_experts) return false;
     if (!(s->swiglu_limit > 0.f) || !(s->swiglu_alpha > 0.f)) return false;
@@ -781,7 +982,7 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 struct Ptrs {
     int32_t *hdr, *counts_hot, *counts, *offsets, *topk_i, *local_ids, *row_token;
     Tile *tiles;
-    uint16_t *logits, *topk_w, *act, *slots;
+    uint16_t *logits, *topk_w, *act, *slots, *xg;
     int32_t *row_slot;
     float *row_w;
 };
@@ -802,6 +1003,7 @@ Ptrs ws_ptrs(const WsLayout &L, void *ws) {
     p.row_w = (float *)(b + L.row_w);
     p.row_slot = (int32_t *)(b + L.row_slot);
     p.act = (uint16_t *)(b + L.act);
+    p.xg = (uint16_t *)(b + L.xg);
     p.slots = (uint16_t *)(b + L.slots);
     return p;
 }
@@ -835,15 +1037,39 @@ int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const u
     int nthreads_ref = 1;
     while (nthreads_ref < s->n_experts) nthreads_ref <<= 1;
     nthreads_ref = nthreads_ref < 64 ? 64 : (nthreads_ref > 512 ? 512 : nthreads_ref);
-    const int grid = (T + kRouteTokens - 1) / kRouteTokens;
-    hipLaunchKernelGGL(route_kernel, dim3(grid), dim3(256), 0, st, x, w->router_w, w->router_b,
-                       fi, fw, T, s->hidden, s->n_experts, s->top_k, p.logits, p.topk_i, p.topk_w,
+    const int H = s->hidden, E = s->n_experts;
+    if (fi == nullptr) {
+        // register tile per 16-lane group: the largest that still gives >= 2048 waves
+        auto groups = [&](int tt, int ee) { return (long)((T + tt - 1) / tt) * ((E + ee - 1) / ee); };
+        auto blocks = [&](long g) { return dim3((unsigned)((g + 15) / 16)); };
+        if (groups(4, 8) >= 8192)
+            hipLaunchKernelGGL((router_kernel<4, 8>), blocks(groups(4, 8)), dim3(256), 0, st, x,
+                               w->router_w, T, H, E, p.logits);
+        else if (groups(2, 4) >= 8192)
+            hipLaunchKernelGGL((router_kernel<2, 4>), blocks(groups(2, 4)), dim3(256), 0, st, x,
+                               w->router_w, T, H, E, p.logits);
+        else if (groups(2, 2) >= 8192)
+            hipLaunchKernelGGL((router_kernel<2, 2>), blocks(groups(2, 2)), dim3(256), 0, st, x,
+                               w->router_w, T, H, E, p.logits);
+        else
+            hipLaunchKernelGGL((router_kernel<1, 1>), blocks(groups(1, 1)), dim3(256), 0, st, x,
+                               w->router_w, T, H, E, p.logits);
+    }
+    hipLaunchKernelGGL(topk_kernel, dim3((T + kTopkTokens - 1) / kTopkTokens), dim3(256), 0, st,
+                       p.logits, w->router_b, fi, fw, T, E, s->top_k, p.topk_i, p.topk_w,
                        p.local_ids, p.counts_hot, p.counts, p.offsets, p.tiles, p.hdr,
                        nthreads_ref);
     if (mk) mk->mark(st);
     hipLaunchKernelGGL(index_kernel, dim3(s->n_experts), dim3(256), 0, st, p.topk_i, p.topk_w, T,
-                       s->top_k, s->n_experts, p.offsets, p.local_ids, p.row_token, p.row_w,
-                       p.row_slot);
+                       s->top_k, s->n_experts, s->hidden, p.offsets, x, p.local_ids, p.row_token,
+                       p.row_w, p.row_slot, p.xg);
+    {
+        long rows = (long)T * s->top_k;
+        long g = (rows * (s->hidden / 8) + 255) / 256;
+        if (g > 4L * device_cus()) g = 4L * device_cus();
+        hipLaunchKernelGGL(gather_kernel, dim3((unsigned)g), dim3(256), 0, st, x, p.row_token,
+                           p.offsets, s->n_experts, s->hidden, p.xg);
+    }
     if (mk) mk->mark(st);
     return hip_status(hipGetLastError());
 }
@@ -852,12 +1078,11 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
                    uint16_t *out, int T, unsigned flags, const WsLayout &L, const Ptrs &p,
                    hipStream_t st, Marks *mk = nullptr) {
     const int H = s->hidden, D = s->intermediate;
-    const int occupancy = 2;
-    const int cap = device_cus() * occupancy;
+    const int cap = device_cus() / 8 * 8;  // one 8-wave workgroup per CU, all XCDs alike
 
     GemmArgs a1;
     memset(&a1, 0, sizeof(a1));
-    a1.A = x;
+    a1.A = p.xg;
     a1.row_token = p.row_token;
     a1.row_slot = p.row_slot;
     a1.Wq = w->w1;
@@ -872,8 +1097,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a1.alpha = s->swiglu_alpha;
     const int max_tiles = (int)((size_t)T * s->top_k / 16 + s->n_experts + 1);
     const int items1 = max_tiles * ((2 * D + kBlockN - 1) / kBlockN);
-    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(items1 < cap ? items1 : cap), dim3(256), 0,
-                       st, a1);
+    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(512), 0, st, a1);
     if (mk) mk->mark(st);
 
     GemmArgs a2 = a1;
@@ -886,8 +1110,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a2.N = H;
     a2.K = D;
     const int items2 = max_tiles * ((H + kBlockN - 1) / kBlockN);
-    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(items2 < cap ? items2 : cap), dim3(256), 0,
-                       st, a2);
+    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(512), 0, st, a2);
     if (mk) mk->mark(st);
 
     const size_t n8 = (size_t)T * H / 8;

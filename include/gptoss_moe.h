@@ -43,8 +43,8 @@ extern "C" {
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {
-    int hidden;        /* H = Config.hidden_dim; multiple of 32 */
-    int intermediate;  /* D = Config.intermediate_dim; multiple of 32 */
+    int hidden;        /* H = Config.hidden_dim; multiple of 64 */
+    int intermediate;  /* D = Config.intermediate_dim; multiple of 64 */
     int n_experts;     /* E = Config.n_experts; 1..256 */
     int top_k;         /* k = Config.experts_per_token; 1..8, <= E */
     float swiglu_limit; /* Config.swiglu_limit (7.0 for gpt-oss) */

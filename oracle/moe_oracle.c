@@ -92,28 +92,28 @@ void orc_dequant_mxfp4_f32(const uint8_t *packed, const uint8_t *scales, int64_t
  * accumulation and no bias (matmul_vec128_singlebuf_Abf16, matmul.hpp:1344,
  * called at getp_run.cpp:2612-2620).  The reference accumulates inside MFMA
  * tiles in an unspecified order; this build pins one fp32 order so router
- * indices can be compared bit for bit: 64 partial sums p[l], each a chain of
- * fmaf over k = 512*i + 8*l + j (i ascending, then j = 0..7), then a
- * butterfly p[l] = p[l] + p[l ^ s] for s = 32, 16, 8, 4, 2, 1.
+ * indices can be compared bit for bit: 16 partial sums p[l], each a chain of
+ * fmaf over k = 128*i + 8*l + j (i ascending, then j = 0..7), then a
+ * butterfly p[l] = p[l] + p[l ^ s] for s = 8, 4, 2, 1.
  * H must be a multiple of 8.
  */
 void orc_router_logits(const uint16_t *x, const uint16_t *wr, int T, int H, int E,
                        uint16_t *out) {
 #pragma omp parallel for schedule(static)
     for (int t = 0; t < T; ++t) {
-        float p[64], q[64];
+        float p[16], q[16];
         for (int e = 0; e < E; ++e) {
             const uint16_t *xr = x + (int64_t)t * H;
             const uint16_t *wrow = wr + (int64_t)e * H;
-            for (int l = 0; l < 64; ++l) {
+            for (int l = 0; l < 16; ++l) {
                 float acc = 0.0f;
-                for (int base = 8 * l; base < H; base += 512)
+                for (int base = 8 * l; base < H; base += 128)
                     for (int j = 0; j < 8; ++j)
                         acc = fmaf(orc_bf2f(xr[base + j]), orc_bf2f(wrow[base + j]), acc);
                 p[l] = acc;
             }
-            for (int s = 32; s >= 1; s >>= 1) {
-                for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ s];
+            for (int s = 8; s >= 1; s >>= 1) {
+                for (int l = 0; l < 16; ++l) q[l] = p[l] + p[l ^ s];
                 memcpy(p, q, sizeof(p));
             }
             out[(int64_t)t * E + e] = orc_f2bf(p[0]);

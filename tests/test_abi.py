@@ -44,7 +44,8 @@ def test_workspace_size():
 
 
 @pytest.mark.parametrize("bad", [
-    dict(hidden=2880 + 16), dict(intermediate=100), dict(n_experts=0), dict(n_experts=257),
+    dict(hidden=2880 + 16), dict(hidden=2880 + 32), dict(intermediate=100), dict(n_experts=0),
+    dict(n_experts=257),
     dict(top_k=0), dict(top_k=9), dict(n_experts=2, top_k=3)])
 def test_invalid_shapes_rejected(bad):
     kw = dict(hidden=2880, intermediate=2880, n_experts=32, top_k=4)
@@ -81,7 +82,7 @@ def test_argument_errors_without_gpu():
     assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
                                   2, fake, need, 8, None) == gm.ERR_INVALID_ARG
     # hidden beyond the router's register budget
-    big = gm.make_shape(4096 + 32, 128, 4, 2)
+    big = gm.make_shape(4096 + 64, 128, 4, 2)
     assert lib.gptoss_moe_route(ctypes.byref(big), ctypes.byref(w), None, 4, None, None, fake,
                                 1 << 40, 8, None) == gm.ERR_UNSUPPORTED
     assert lib.gptoss_moe_rmsnorm(None, None, None, 1, 8, None) == gm.ERR_INVALID_ARG

@@ -79,23 +79,23 @@ def test_dequant_nibble_order():
 
 # --------------------------------------------------------------- router --
 def _router_f32_emulation(x, wr):
-    """The pinned fp32 order written with numpy float32: 64 lane partials over
-    k = 512 i + 8 l + j, then an xor butterfly.  bf16 x bf16 products are exact
+    """The pinned fp32 order written with numpy float32: 16 partials over
+    k = 128 i + 8 l + j, then an xor butterfly.  bf16 x bf16 products are exact
     in fp32, so fmaf(a, b, acc) == float32(acc + a*b)."""
     xf, wf = bf16_to_f32(x), bf16_to_f32(wr)
     T, H = xf.shape
     E = wf.shape[0]
     prod = xf[:, None, :] * wf[None, :, :]       # exact, [T][E][H]
-    p = np.zeros((T, E, 64), np.float32)
-    for base in range(0, H, 512):
+    p = np.zeros((T, E, 16), np.float32)
+    for base in range(0, H, 128):
         for j in range(8):
-            k = base + 8 * np.arange(64) + j
+            k = base + 8 * np.arange(16) + j
             ok = k < H
-            add = np.zeros((T, E, 64), np.float32)
+            add = np.zeros((T, E, 16), np.float32)
             add[:, :, ok] = prod[:, :, k[ok]]
             p = (p + add).astype(np.float32)
-    lanes = np.arange(64)
-    for s in (32, 16, 8, 4, 2, 1):
+    lanes = np.arange(16)
+    for s in (8, 4, 2, 1):
         p = (p + p[:, :, lanes ^ s]).astype(np.float32)
     return f32_to_bf16(p[:, :, 0])
 
