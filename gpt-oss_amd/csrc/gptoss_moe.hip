@@ -32,7 +32,7 @@ constexpr int kWave = 64;
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 8;
 constexpr int kMaxHidden = 4096;    // router keeps x rows in registers
-constexpr int kTileRows = 64;       // rows per grouped-GEMM tile (4 x 16)
+constexpr int kTileRows = 32;       // rows per grouped-GEMM tile (2 x 16)
 constexpr int kBlockN = 128;        // weight rows per workgroup (4 waves x 32)
 constexpr int kChunkK = 256;        // k per LDS chunk of activations
 constexpr int kUnits = kChunkK / 8; // 16-byte units per LDS row
@@ -75,7 +75,21 @@ struct WsLayout {
 
 // hdr ints: DONE = workgroups finished (reset by the last one), NTILES = tile
 // count, STATUS_HOT = dropped slots of the running call, STATUS = last call's.
-enum { HDR_DONE = 0, HDR_NTILES = 1, HDR_STATUS_HOT = 2, HDR_STATUS = 4, HDR_INTS = 64 };
+// XSTART / XCOUNT: the tile list is grouped by XCD; tiles of XCD x are
+// tiles[XSTART + x] .. + [XCOUNT + x].
+enum {
+    HDR_DONE = 0, HDR_NTILES = 1, HDR_STATUS_HOT = 2, HDR_STATUS = 4, HDR_XSTART = 8,
+    HDR_XCOUNT = 16, HDR_INTS = 256
+};
+// Diagnostic builds (-DGPTOSS_TRACE) accumulate per-role cycle counts into the
+// header bytes 512..1023 (64 x u64); the product build compiles this away.
+#ifdef GPTOSS_TRACE
+#define TR_T0 const unsigned long long _tr0 = __builtin_readcyclecounter();
+#define TR_ADD(slot) atomicAdd(reinterpret_cast<unsigned long long *>(const_cast<int32_t *>(a.hdr) + 128) + (slot), __builtin_readcyclecounter() - _tr0);
+#else
+#define TR_T0
+#define TR_ADD(slot)
+#endif
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -203,6 +217,104 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
             const int t = tb * TT + i, e = eb * EE + j;
             if (lane16 == 0 && t < T && e < E) logits[(size_t)t * E + e] = f2bf(v);
         }
+}
+
+// Wave-inclusive scan of v over 64 lanes.
+__device__ __forceinline__ int wave_scan(int v, int lane) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const int o = __shfl_up(v, s, 64);
+        if (lane >= s) v += o;
+    }
+    return v;
+}
+
+// Number of r in [0, n) with r % 8 == x.
+__device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x) / 8 + 1 : 0; }
+
+// One wave: read-and-reset the histogram, write counts and exclusive offsets,
+// and the tile list (kTileRows rows per tile) grouped by XCD.  An expert's
+// tiles are cut into units of up to 2 tiles; the U2 2-tile units are dealt
+// to the 8 XCDs round robin (unit rank r goes to XCD r % 8), then the U1
+// 1-tile units continue the deal.  That balances tiles per XCD within 2,
+// and both tiles of a unit share one XCD's L2 (the GEMM streams the unit's
+// weights once for both).  Tiles of XCD x occupy
+// tiles[xstart(x) .. xstart(x) + xcount(x)), 2-tile units first.
+__device__ void build_tiles(int32_t *counts_hot, int32_t *__restrict__ counts,
+                            int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr,
+                            int E, int lane) {
+    // lane l owns experts 4l .. 4l+3
+    int c[4], nt[4], n2[4], n1[4];
+    int csum = 0, s2 = 0, s1 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        c[j] = e < E ? atomicExch(&counts_hot[e], 0) : 0;
+        nt[j] = (c[j] + kTileRows - 1) / kTileRows;
+        n2[j] = nt[j] / 2;
+        n1[j] = nt[j] % 2;
+        csum += c[j];
+        s2 += n2[j];
+        s1 += n1[j];
+    }
+    const int cinc = wave_scan(csum, lane), i2 = wave_scan(s2, lane), i1 = wave_scan(s1, lane);
+    const int U2 = __shfl(i2, 63, 64), U1 = __shfl(i1, 63, 64);
+    auto xcount = [&](int x) { return 2 * n_mod8(U2, x) + n_mod8(U2 + U1, x) - n_mod8(U2, x); };
+    int xstart[8];
+    {
+        int acc = 0;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            xstart[x] = acc;
+            acc += xcount(x);
+        }
+    }
+    int off = cinc - csum, r2 = i2 - s2, r1 = i1 - s1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        if (e < E) {
+            counts[e] = c[j];
+            offsets[e] = off;
+            for (int m = 0; m < nt[j]; ++m) {
+                const int u = m / 2;
+                int x, pos;  // XCD of the unit and the tile's position in that XCD
+                if (u < n2[j]) {
+                    const int rank = r2 + u;
+                    x = rank & 7;
+                    pos = 2 * (rank / 8) + (m & 1);
+                } else {
+                    const int rank = U2 + r1;
+                    x = rank & 7;
+                    pos = 2 * n_mod8(U2, x) + n_mod8(rank, x) - n_mod8(U2, x);
+                }
+                int base = 0;
+#pragma unroll
+                for (int xx = 0; xx < 8; ++xx)
+                    if (xx == x) base = xstart[xx];
+                Tile tl;
+                tl.expert = e;
+                tl.row0 = off + m * kTileRows;
+                tl.rows = min(kTileRows, c[j] - m * kTileRows);
+                tl.pad = 0;
+                tiles[base + pos] = tl;
+            }
+        }
+        off += c[j];
+        r2 += n2[j];
+        r1 += n1[j];
+    }
+    if (lane == 63) {
+        offsets[E] = off;
+        hdr[HDR_NTILES] = 2 * U2 + U1;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            hdr[HDR_XSTART + x] = xstart[x];
+            hdr[HDR_XCOUNT + x] = xcount(x);
+        }
+        hdr[HDR_STATUS] = atomicExch(&hdr[HDR_STATUS_HOT], 0);
+        hdr[HDR_DONE] = 0;
+    }
 }
 
 constexpr int kTopkTokens = 4;  // one wave per token
@@ -335,51 +447,7 @@ __global__ __launch_bounds__(256) void topk_kernel(
     __syncthreads();
     if (!s_last || wave != 0) return;
     __threadfence();
-    // lane l owns experts 4l .. 4l+3
-    int c[4], nt[4];
-    int csum = 0, tsum = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = 4 * lane + j;
-        c[j] = e < E ? atomicExch(&counts_hot[e], 0) : 0;
-        nt[j] = (c[j] + kTileRows - 1) / kTileRows;
-        csum += c[j];
-        tsum += nt[j];
-    }
-    int cinc = csum, tinc = tsum;
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const int oc = __shfl_up(cinc, s, 64), ot = __shfl_up(tinc, s, 64);
-        if (lane >= s) {
-            cinc += oc;
-            tinc += ot;
-        }
-    }
-    int off = cinc - csum, toff = tinc - tsum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = 4 * lane + j;
-        if (e < E) {
-            counts[e] = c[j];
-            offsets[e] = off;
-            for (int m = 0; m < nt[j]; ++m) {
-                Tile tl;
-                tl.expert = e;
-                tl.row0 = off + m * kTileRows;
-                tl.rows = min(kTileRows, c[j] - m * kTileRows);
-                tl.pad = 0;
-                tiles[toff + m] = tl;
-            }
-        }
-        off += c[j];
-        toff += nt[j];
-    }
-    if (lane == 63) {
-        offsets[E] = off;
-        hdr[HDR_NTILES] = toff;
-        hdr[HDR_STATUS] = atomicExch(&hdr[HDR_STATUS_HOT], 0);
-        hdr[HDR_DONE] = 0;
-    }
+    build_tiles(counts_hot, counts, offsets, tiles, hdr, E, lane);
 }
 
 // Compact row map (route_build_index_kernel_bf16wts, moe.hpp:1173-1270): one
@@ -491,10 +559,12 @@ constexpr int kStageK = 256;     // k per stage (128 B of each weight row)
 constexpr int kAUnits = kTileRows * kUnits;  // 16-byte activation units per stage
 
 struct StageSlot {
-    uint8_t w[4][32 * 128];      // [producer/consumer wave][32 rows x 128 B], swizzled
-    uint8_t s[4][32 * 8];        // scales [wave][row][chunk]
+    uint8_t w[4][32 * 128];      // [consumer wave][32 rows x 128 B], swizzled
     uint4 a[kAUnits];            // activations [row][unit ^ (row & 15)]
 };
+// e8m0 scales of one item: its 128 weight rows x K/32 bytes, copied whole
+// (contiguous in memory) by the consumers one item ahead; double-buffered.
+constexpr int kScaleBytes = kBlockN * (kMaxHidden / 32);
 
 // LDS row (0..31) of the wave's weight row wr (0..31): MLP1 puts gate rows
 // (even) in 0..15 and up rows (odd) in 16..31, so MFMA tile 0 / 1 lane n holds
@@ -505,43 +575,66 @@ __device__ __forceinline__ int lds_row_of(int wr) {
 }
 
 // Work items are (tile, 128-row weight block).  Workgroups are dispatched to
-// the 8 XCDs round robin (workgroup b runs on XCD b % 8), so tile t is given
-// only to XCD t % 8: its activation rows are then re-read by all of its
-// weight blocks from that XCD's L2 instead of being fetched by every XCD.
-// Within an XCD, its Gx workgroups stride over its items.
+// the 8 XCDs round robin (workgroup b runs on XCD b % 8) and the tile list is
+// grouped by XCD, so XCD x only touches its own tiles: their activation rows
+// stay in its L2, and the tiles of one expert (one unit) stream each weight
+// block from the same L2.  Within an XCD, items are weight-block-major
+// (consecutive items are the XCD's tiles at one block), and its Gx
+// workgroups stride over them.
 struct ItemMap {
-    int nblk, xcd, w, Gx;
-    __device__ __forceinline__ void init(int ntiles, int nblk_, int &n_items) {
+    int nblk, xcd, w, Gx, base, ntx;
+    __device__ __forceinline__ void init(const int32_t *hdr, int nblk_, int &n_items) {
         nblk = nblk_;
         xcd = (int)blockIdx.x & 7;
         w = (int)blockIdx.x >> 3;
         Gx = (int)gridDim.x >> 3;
-        const int tiles_x = ntiles > xcd ? (ntiles - xcd + 7) / 8 : 0;
-        const int items_x = tiles_x * nblk;
+        base = hdr[HDR_XSTART + xcd];
+        ntx = hdr[HDR_XCOUNT + xcd];
+        const int items_x = ntx * nblk;
         n_items = items_x > w ? (items_x - w + Gx - 1) / Gx : 0;
     }
     __device__ __forceinline__ void at(const Tile *tiles, int i, Tile &tl, int &nb) const {
         const int ii = w + i * Gx;
-        tl = tiles[xcd + 8 * (ii / nblk)];
-        nb = ii % nblk;
+        nb = ii / ntx;
+        tl = tiles[base + ii - nb * ntx];
     }
 };
 
-// Step st of this workgroup's stream -> item tile, weight block and stage.
-__device__ __forceinline__ void step_at(const GemmArgs &a, const ItemMap &im, int NST, int st,
-                                        Tile &tl, int &nb, int &j) {
-    const int i = st / NST;
-    j = st - i * NST;
-    im.at(a.tiles, i, tl, nb);
-}
+// Step -> (item tile, weight block, stage) for a role that walks its steps in
+// order.  The next item's descriptor is fetched one item ahead, so the scalar
+// load's latency is never exposed on a stage.
+struct StepCursor {
+    int cur, n_items;
+    Tile tl, ntl;
+    int nb, nnb;
+    __device__ __forceinline__ void init(const GemmArgs &a, const ItemMap &im, int n) {
+        n_items = n;
+        cur = -1;
+        im.at(a.tiles, 0, ntl, nnb);
+    }
+    __device__ __forceinline__ void at(const GemmArgs &a, const ItemMap &im, int NST, int st,
+                                       Tile &t, int &b, int &j) {
+        const int i = st / NST;
+        j = st - i * NST;
+        if (i != cur) {  // uniform; only scalar loads inside
+            cur = i;
+            tl = ntl;
+            nb = nnb;
+            im.at(a.tiles, min(i + 1, n_items - 1), ntl, nnb);
+        }
+        t = tl;
+        b = nb;
+    }
+};
 
 // Weight producer (waves 4, 5): rows 64 p .. 64 p + 63 of the block, 8 load
 // instructions of 8 rows x one full 128-byte row chunk per stage (lane l: row
-// 8 t + (l >> 3), chunk l & 7), plus the stage's 8 e8m0 bytes of row l as
-// four 2-byte loads (a row's scales are K / 32 bytes apart, so 2-byte
-// aligned).  12 load instructions per stage keep kWDepth stages within the
-// 63 outstanding loads a wave can track.  Invalid lanes write zeros.
-constexpr int kWDepth = 4;
+// 8 t + (l >> 3), chunk l & 7); kWDepth stages in flight (within the 63
+// outstanding loads a wave can track).  Invalid lanes write zeros.
+#ifndef GPTOSS_WDEPTH
+#define GPTOSS_WDEPTH 5
+#endif
+constexpr int kWDepth = GPTOSS_WDEPTH;
 template <bool kMlp1>
 __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slots, int total,
                                                int total_p, const ItemMap &im, int NST) {
@@ -549,18 +642,18 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
     const int rr = lane >> 3, ch = lane & 7;
     const int N = a.N, K = a.K;
     uint4 q[kWDepth][8];
-    uint32_t sc[kWDepth][4];  // bytes 2 m, 2 m + 1 of row `lane`'s stage scales
     int stage_of[kWDepth];
     bool wval_of[kWDepth][2];
+    StepCursor cursor;
+    cursor.init(a, im, total / NST);
 
     auto issue = [&](int st, int r) {
         st = min(st, total - 1);
         Tile tl;
         int nb, j;
-        step_at(a, im, NST, st, tl, nb, j);
+        cursor.at(a, im, NST, st, tl, nb, j);
         const size_t seg_el = (size_t)N * K;
         const uint8_t *wq = a.Wq + (size_t)tl.expert * (seg_el / 2);
-        const uint8_t *ws = a.Ws + (size_t)tl.expert * (seg_el / 32);
         const uint32_t k = (uint32_t)min(j * kStageK + 32 * ch, K - 32);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {  // consumer region 2 p + hh
@@ -574,15 +667,6 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
                 q[r][4 * hh + t] = *reinterpret_cast<const uint4 *>(wq + el / 2);
             }
         }
-        // scales: lane = row (64 p + lane) of the block, bytes 8 j .. 8 j + 7 of
-        // its K / 32 scale bytes; each 2-byte load is clamped inside the row
-        // (K / 32 is even, so every load is 2-byte aligned)
-        const int srow = min(nb * kBlockN + 64 * p + lane, N - 1);
-        const uint32_t sb = (uint32_t)srow * (uint32_t)(K / 32);
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-            sc[r][m] = *reinterpret_cast<const uint16_t *>(
-                ws + sb + (uint32_t)min(j * 8 + 2 * m, K / 32 - 2));
         stage_of[r] = j;
     };
     // Masks instead of selects: a select on loaded data becomes a branch with
@@ -600,15 +684,6 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
                     make_uint4(v.x & km, v.y & km, v.z & km, v.w & km);
             }
         }
-        // scale bytes of row `lane` (region 2 p + lane / 32, row lane % 32), chunks
-        // past K zeroed; rows past N are never read by a live output column
-        const int wr = lane & 31;
-        const int lr = lds_row_of<kMlp1>(wr);
-        const int kc = (K - stage_of[r] * kStageK) / 32;  // live chunks in this stage
-        uint32_t lo = sc[r][0] | (sc[r][1] << 16), hi = sc[r][2] | (sc[r][3] << 16);
-        const uint64_t keep = kc >= 8 ? ~0ull : ((1ull << (8 * kc)) - 1ull);
-        const uint64_t v64 = (((uint64_t)hi << 32) | lo) & keep;
-        *reinterpret_cast<uint64_t *>(&sl.s[2 * p + (lane >> 5)][lr * 8]) = v64;
     };
 
 #pragma unroll
@@ -622,58 +697,88 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
             // keep each step's use of its loads from being hoisted above the
             // previous barrier (it would wait for every load in flight)
             __builtin_amdgcn_sched_barrier(0);
-            write(r, slots[(s0 + r) & 1]);
-            issue(s0 + r + kWDepth, r);
+            {
+                TR_T0
+                write(r, slots[(s0 + r) & 1]);
+                TR_ADD((kMlp1 ? 0 : 16) + 0)
+            }
+            {
+                TR_T0
+                issue(s0 + r + kWDepth, r);
+                TR_ADD((kMlp1 ? 0 : 16) + 1)
+            }
             __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();
+            {
+                TR_T0
+                __syncthreads();
+                TR_ADD((kMlp1 ? 0 : 16) + 2)
+            }
         }
     }
     __syncthreads();  // iteration total_p: consumers finish the last step
 }
 
-// Activation loader (waves 6, 7): rows 32 p' .. 32 p' + 31 of the 64-row
-// activation chunk (lane l, unit i: row 2 i + (l >> 5), 16-byte unit l & 31,
-// two full 512-byte row chunks per instruction), one stage ahead.  Rows past
-// the tile repeat its last row and k past K repeats the last unit: finite
-// values that meet zero weights or discarded output rows.
-__device__ __forceinline__ void aload_stage(const GemmArgs &a, const ItemMap &im, int NST,
-                                            int total, int st, int p, int lane, u32x4 (&v)[16]) {
-    st = min(st, total - 1);
-#if defined(GPTOSS_DIAG) && GPTOSS_DIAG == 1
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = u32x4{(uint32_t)st, 1u, 2u, 3u};
-    return;
-#endif
-    Tile tl;
-    int nb, j;
-    step_at(a, im, NST, st, tl, nb, j);
-    const int K = a.K;
-    const int k = min(j * kStageK + 8 * (lane & 31), K - 8);
-    const uint16_t *base = a.A + (size_t)tl.row0 * K + k;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int row = min(32 * p + 2 * i + (lane >> 5), tl.rows - 1);
-        v[i] = *reinterpret_cast<const u32x4 *>(base + (uint32_t)row * (uint32_t)K);
-    }
-}
-
+// Activation loader (waves 6, 7): the stage's 32 x 256 activation chunk;
+// instruction i of loader p covers rows 4 i + 2 p + (0, 1) (two full 512-byte
+// row chunks; lane l: row + (l >> 5), 16-byte unit l & 31).  Loads are issued
+// kADepth stages ahead, as deep as the weights: the CU returns loads in
+// order, so an activation load issued later than the weights it meets would
+// wait behind them.  Rows past the tile repeat its last row (finite data that
+// only meets output rows the epilogue drops); k past K repeats the last unit
+// against zero weights.
+constexpr int kADepth = kWDepth;
 __device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots, int total,
                                              int total_p, const ItemMap &im, int NST) {
     const int p = (threadIdx.x >> 6) - 6, lane = threadIdx.x & 63;
     const int c = lane & 31;
-    u32x4 v[16];
-    aload_stage(a, im, NST, total, 0, p, lane, v);
-    for (int s = 0; s < total_p; ++s) {
-        __builtin_amdgcn_sched_barrier(0);
-        StageSlot &sl = slots[s & 1];
+    const int K = a.K;
+    u32x4 v[kADepth][8];
+    StepCursor cursor;
+    cursor.init(a, im, total / NST);
+    auto issue = [&](int st, int r) {
+        st = min(st, total - 1);
+        Tile tl;
+        int nb, j;
+        cursor.at(a, im, NST, st, tl, nb, j);
+        const int k = min(j * kStageK + 8 * c, K - 8);
+        const uint16_t *base = a.A + (size_t)tl.row0 * K + k;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int row = 32 * p + 2 * i + (lane >> 5);
-            *reinterpret_cast<u32x4 *>(&sl.a[row * kUnits + (c ^ (row & 15))]) = v[i];
+        for (int i = 0; i < 8; ++i) {
+            const int row = min(4 * i + 2 * p + (lane >> 5), tl.rows - 1);
+            v[r][i] = *reinterpret_cast<const u32x4 *>(base + (uint32_t)row * (uint32_t)K);
         }
-        aload_stage(a, im, NST, total, s + 1, p, lane, v);
+    };
+#pragma unroll
+    for (int r = 0; r < kADepth; ++r) {
+        issue(r, r);
         __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
+    }
+    for (int s0 = 0; s0 < total_p; s0 += kADepth) {
+#pragma unroll
+        for (int r = 0; r < kADepth; ++r) {
+            __builtin_amdgcn_sched_barrier(0);
+            StageSlot &sl = slots[(s0 + r) & 1];
+            {
+                TR_T0
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int row = 4 * i + 2 * p + (lane >> 5);
+                    *reinterpret_cast<u32x4 *>(&sl.a[row * kUnits + (c ^ (row & 15))]) = v[r][i];
+                }
+                TR_ADD(32 + 0)
+            }
+            {
+                TR_T0
+                issue(s0 + r + kADepth, r);
+                TR_ADD(32 + 1)
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                TR_T0
+                __syncthreads();
+                TR_ADD(32 + 2)
+            }
+        }
     }
     __syncthreads();
 }
@@ -682,19 +787,43 @@ __device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots
 // epilogue.  MT (row tiles of 16) is a template parameter so the
 // accumulators are plain registers with no guarded MFMAs (a guard around an
 // MFMA makes the compiler copy its accumulator in and out).
+// Item i's scale block: weight rows nb*128 .. +127 (those below N) of its
+// expert, K/32 bytes each, contiguous; 4 x 16 bytes per consumer lane.
+__device__ __forceinline__ void scale_block_load(const GemmArgs &a, const Tile &tl, int nb,
+                                                 u32x4 (&v)[4]) {
+    const int N = a.N, K = a.K;
+    const int nrows = min(kBlockN, N - nb * kBlockN);
+    const int len = nrows * (K / 32);  // multiple of 64 bytes
+    const uint8_t *src = a.Ws + (size_t)tl.expert * ((size_t)N * K / 32) +
+                         (size_t)nb * kBlockN * (K / 32);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        v[u] = *reinterpret_cast<const u32x4 *>(src + min(16 * ((int)threadIdx.x + 256 * u), len - 16));
+}
+__device__ __forceinline__ void scale_block_store(uint8_t *dst, const u32x4 (&v)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        *reinterpret_cast<u32x4 *>(dst + 16 * ((int)threadIdx.x + 256 * u)) = v[u];
+}
+
 template <int MT, bool kMlp1>
 __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot *slots, int &s,
-                                             const Tile &tl, int nb, int NST) {
+                                             const Tile &tl, int nb, int NST,
+                                             const uint8_t *scales, uint8_t *next_scales,
+                                             bool has_next, const Tile &ntl, int nnb) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n_l = lane & 15, g = lane >> 4;
     const int N = a.N;
+    const int KS = a.K / 32;
+    u32x4 nsv[4];
+    if (has_next) scale_block_load(a, ntl, nnb, nsv);
     f32x4 acc[MT][2];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < NST; ++j, ++s) {
+        TR_T0
         const StageSlot &sl = slots[s & 1];
         const uint8_t *wb = sl.w[wave];
-        const uint8_t *sb = sl.s[wave];
 #if defined(GPTOSS_DIAG) && GPTOSS_DIAG == 2
         {
             const uint4 v = sl.a[lane * 16];
@@ -713,7 +842,9 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
             for (int tt = 0; tt < 2; ++tt) {
                 const int lr = 16 * tt + n_l, c = g + 4 * h;
                 wv[tt] = *reinterpret_cast<const uint4 *>(wb + lr * 128 + 16 * (c ^ (lr & 7)));
-                se[tt] = sb[lr * 8 + c];
+                // weight row of LDS row lr within the block (inverse of lds_row_of)
+                const int wr = wave * 32 + (kMlp1 ? 2 * n_l + tt : lr);
+                se[tt] = (8 * j + c < KS) ? scales[wr * KS + 8 * j + c] : 0u;
                 if (se[tt] == 0) {  // e8m0 = 0 -> +-0 (code * 0.0 in the reference); rare
                     wv[tt].x &= 0x88888888u;
                     wv[tt].y &= 0x88888888u;
@@ -794,25 +925,41 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
                 }
             }
         }
-        __syncthreads();
+        if (j == NST - 1 && has_next) scale_block_store(next_scales, nsv);
+        TR_ADD((kMlp1 ? 48 : 56) + 0)
+        {
+            TR_T0
+            __syncthreads();
+            TR_ADD((kMlp1 ? 48 : 56) + 2)
+        }
     }
 }
 
 template <bool kMlp1>
-__device__ __forceinline__ void gemm_consumer(const GemmArgs &a, StageSlot *slots, int n_items,
+__device__ __forceinline__ void gemm_consumer(const GemmArgs &a, StageSlot *slots,
+                                              uint8_t (*sscale)[kScaleBytes], int n_items,
                                               int total_p, const ItemMap &im, int NST) {
-    __syncthreads();  // iteration 0: producers fill stage 0
+    Tile tl, ntl;
+    int nb, nnb;
+    im.at(a.tiles, 0, tl, nb);
+    {
+        u32x4 v[4];
+        scale_block_load(a, tl, nb, v);
+        scale_block_store(sscale[0], v);
+    }
+    __syncthreads();  // iteration 0: producers fill stage 0; item 0's scales land
     int s = 0;
     for (int i = 0; i < n_items; ++i) {
-        Tile tl;
-        int nb;
-        im.at(a.tiles, i, tl, nb);
-        switch ((tl.rows + 15) / 16) {
-            case 1: consume_item<1, kMlp1>(a, slots, s, tl, nb, NST); break;
-            case 2: consume_item<2, kMlp1>(a, slots, s, tl, nb, NST); break;
-            case 3: consume_item<3, kMlp1>(a, slots, s, tl, nb, NST); break;
-            default: consume_item<4, kMlp1>(a, slots, s, tl, nb, NST); break;
-        }
+        const bool has_next = i + 1 < n_items;
+        im.at(a.tiles, min(i + 1, n_items - 1), ntl, nnb);
+        if (tl.rows <= 16)
+            consume_item<1, kMlp1>(a, slots, s, tl, nb, NST, sscale[i & 1], sscale[(i + 1) & 1],
+                                   has_next, ntl, nnb);
+        else
+            consume_item<2, kMlp1>(a, slots, s, tl, nb, NST, sscale[i & 1], sscale[(i + 1) & 1],
+                                   has_next, ntl, nnb);
+        tl = ntl;
+        nb = nnb;
     }
     for (; s < total_p; ++s) __syncthreads();  // producers' padding steps
 }
@@ -820,17 +967,17 @@ __device__ __forceinline__ void gemm_consumer(const GemmArgs &a, StageSlot *slot
 template <bool kMlp1>
 __global__ __launch_bounds__(512) void grouped_gemm_kernel(GemmArgs a) {
     __shared__ StageSlot slots[2];
-    const int ntiles = a.hdr[HDR_NTILES];
+    __shared__ __attribute__((aligned(16))) uint8_t sscale[2][kScaleBytes];
     ItemMap im;
     int n_items;
-    im.init(ntiles, (a.N + kBlockN - 1) / kBlockN, n_items);
+    im.init(a.hdr, (a.N + kBlockN - 1) / kBlockN, n_items);
     const int NST = (a.K + kStageK - 1) / kStageK;
     if (n_items == 0) return;
     const int total = n_items * NST;
     const int total_p = (total + kWDepth - 1) / kWDepth * kWDepth;
     const int wave = threadIdx.x >> 6;
     if (wave < 4)
-        gemm_consumer<kMlp1>(a, slots, n_items, total_p, im, NST);
+        gemm_consumer<kMlp1>(a, slots, sscale, n_items, total_p, im, NST);
     else if (wave < 6)
         gemm_wproducer<kMlp1>(a, slots, total, total_p, im, NST);
     else
@@ -1011,7 +1158,8 @@ Ptrs ws_ptrs(const WsLayout &L, void *ws) {
 int check_common(const gptoss_moe_shape *shape, const gptoss_moe_weights *w, int n_tokens,
                  const int32_t *fi, const uint16_t *fw, void *ws, size_t ws_bytes, int max_tokens) {
     if (!shape_ok(shape) || !w) return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (shape->hidden > kMaxHidden) return GPTOSS_MOE_ERR_UNSUPPORTED;
+    if (shape->hidden > kMaxHidden || shape->intermediate > kMaxHidden)
+        return GPTOSS_MOE_ERR_UNSUPPORTED;
     if (n_tokens < 0 || max_tokens < 0 || n_tokens > max_tokens) return GPTOSS_MOE_ERR_INVALID_ARG;
     if ((fi == nullptr) != (fw == nullptr)) return GPTOSS_MOE_ERR_INVALID_ARG;
     if (fi == nullptr && (!w->router_w || !w->router_b || !aligned16(w->router_w)))

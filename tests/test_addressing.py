@@ -1,8 +1,8 @@
 """Bounds of every global load the grouped GEMM issues, evaluated on the CPU
 for many shapes (regression test: a clamp that went negative for K < 256
 once put a scale load outside its buffer).  The index arithmetic below is
-the kernel's (gpt-oss_amd/csrc/gptoss_moe.hip, gemm_wproducer and
-aload_stage), vectorised over lanes, stages and rows."""
+the kernel's (gpt-oss_amd/csrc/gptoss_moe.hip, gemm_wproducer,
+gemm_aloader and scale_block_load), vectorised over lanes, stages and rows."""
 import numpy as np
 import pytest
 
@@ -11,10 +11,12 @@ STAGE_K = 256
 
 
 def wproducer_loads(N, K):
-    """(byte offsets into one expert's nibbles, byte offsets into its scales)."""
+    """Byte offsets of the weight producer's 16-byte nibble loads into one
+    expert's N*K/2 bytes (gemm_wproducer: lane l loads row 8 t + (l >> 3),
+    chunk l & 7; invalid row blocks read row 0)."""
     nst = (K + STAGE_K - 1) // STAGE_K
     nblk = (N + BLOCK_N - 1) // BLOCK_N
-    q, s = [], []
+    q = []
     lane = np.arange(64)
     rr, ch = lane >> 3, lane & 7
     for nb in range(nblk):
@@ -27,42 +29,104 @@ def wproducer_loads(N, K):
                     el0 = np.where(wvalid, row0 + rr, 0) * K + k
                     for t in range(4):
                         q.append((el0 + t * 8 * K) // 2)
-                srow = np.minimum(nb * BLOCK_N + 64 * p + lane, N - 1)
-                for m in range(4):
-                    s.append(srow * (K // 32) + np.minimum(j * 8 + 2 * m, K // 32 - 2))
-    return np.concatenate(q), np.concatenate(s)
+    return np.concatenate(q)
 
 
-def aloader_loads(K, row0, rows, P):
+def scale_block_loads(N, K):
+    """Byte offsets of the consumers' 16-byte loads of one item's scale block
+    (scale_block_load: 256 consumer threads x 4 loads, clamped to the block)."""
+    out = []
+    tid = np.arange(256)
+    for nb in range((N + BLOCK_N - 1) // BLOCK_N):
+        nrows = min(BLOCK_N, N - nb * BLOCK_N)
+        length = nrows * (K // 32)
+        # the block must fit the LDS copy the consumers read from
+        assert length <= 4 * 256 * 16
+        for u in range(4):
+            out.append(nb * BLOCK_N * (K // 32) + np.minimum(16 * (tid + 256 * u), length - 16))
+    return np.concatenate(out)
+
+
+def aloader_loads(K, row0, rows):
+    """Element offsets of the activation loader's 8-element loads (gemm_aloader:
+    instruction i of loader p covers rows 4 i + 2 p + (l >> 5), unit l & 31;
+    rows past the tile repeat its last row)."""
     nst = (K + STAGE_K - 1) // STAGE_K
     lane = np.arange(64)
     out = []
     for p in range(2):
         for j in range(nst):
             k = np.minimum(j * STAGE_K + 8 * (lane & 31), K - 8)
-            for i in range(16):
-                row = np.minimum(32 * p + 2 * i + (lane >> 5), rows - 1)
+            for i in range(8):
+                row = np.minimum(4 * i + 2 * p + (lane >> 5), rows - 1)
                 out.append((row0 + row) * K + k)
     return np.concatenate(out)
 
 
 @pytest.mark.parametrize("N,K", [(256, 128), (128, 128), (64, 64), (5760, 2880), (2880, 2880),
-                                 (128, 64), (192, 320), (320, 192)])
+                                 (128, 64), (192, 320), (320, 192), (8192, 4096), (4096, 4096)])
 def test_weight_and_scale_loads_in_bounds(N, K):
-    q, s = wproducer_loads(N, K)
-    # 16-byte nibble loads inside the expert's N*K/2 bytes, 2-byte scale loads
-    # inside its N*K/32 bytes and 2-byte aligned
+    q = wproducer_loads(N, K)
+    s = scale_block_loads(N, K)
+    # 16-byte loads inside the expert's N*K/2 nibble bytes and N*K/32 scale bytes
     assert q.min() >= 0 and (q + 16).max() <= N * K // 2
     assert (q % 16 == 0).all()
-    assert s.min() >= 0 and (s + 2).max() <= N * K // 32
-    assert (s % 2 == 0).all()
+    assert s.min() >= 0 and (s + 16).max() <= N * K // 32
+    assert (s % 16 == 0).all()
 
 
 @pytest.mark.parametrize("K", [64, 128, 192, 2880])
-@pytest.mark.parametrize("rows", [1, 15, 16, 33, 64])
+@pytest.mark.parametrize("rows", [1, 15, 16, 31, 32])
 def test_activation_loads_in_bounds(K, rows):
     P = 97  # compact rows in the buffer; the tile is the last `rows` of them
     row0 = P - rows
-    a = aloader_loads(K, row0, rows, P)
+    a = aloader_loads(K, row0, rows)
     assert a.min() >= 0 and (a + 8).max() <= P * K  # 8 bf16 per load
     assert (a % 8 == 0).all()
+
+
+def n_mod8(n, x):
+    return (n - 1 - x) // 8 + 1 if n > x else 0
+
+
+def build_tiles(counts, tile_rows=32):
+    """The placement of build_tiles (gptoss_moe.hip): returns {pos: (e, m)} and
+    per-XCD (start, count)."""
+    nt = [(c + tile_rows - 1) // tile_rows for c in counts]
+    n2 = [t // 2 for t in nt]
+    n1 = [t % 2 for t in nt]
+    U2, U1 = sum(n2), sum(n1)
+    xcount = [2 * n_mod8(U2, x) + n_mod8(U2 + U1, x) - n_mod8(U2, x) for x in range(8)]
+    xstart = list(np.concatenate([[0], np.cumsum(xcount)[:-1]]))
+    placed, unit_xcd = {}, {}
+    r2 = r1 = 0
+    for e, t in enumerate(nt):
+        for m in range(t):
+            u = m // 2
+            if u < n2[e]:
+                rank = r2 + u
+                x, pos = rank & 7, 2 * (rank // 8) + (m & 1)
+            else:
+                rank = U2 + r1
+                x = rank & 7
+                pos = 2 * n_mod8(U2, x) + n_mod8(rank, x) - n_mod8(U2, x)
+            assert 0 <= pos < xcount[x]
+            assert xstart[x] + pos not in placed
+            placed[xstart[x] + pos] = (e, m)
+            unit_xcd.setdefault((e, u), set()).add(x)
+        r2 += n2[e]
+        r1 += n1[e]
+    return placed, xcount, unit_xcd
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_tile_placement_is_a_balanced_bijection(seed):
+    rng = np.random.default_rng(seed)
+    E = int(rng.choice([4, 32, 128, 256]))
+    counts = rng.integers(0, 200 if seed % 2 else 70, E)
+    counts[rng.random(E) < 0.2] = 0
+    placed, xcount, unit_xcd = build_tiles(counts)
+    total = sum((c + 31) // 32 for c in counts)
+    assert sorted(placed) == list(range(total))
+    assert max(xcount) - min(xcount) <= 2
+    assert all(len(v) == 1 for v in unit_xcd.values())  # a unit's tiles share an XCD
