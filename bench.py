@@ -39,7 +39,45 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=20)
+    ap.add_argument("--traffic", default="",
+                    help="HBM traffic summary (default profiles/hbm_traffic_<config>.txt)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy 3 times (counter calibration)")
     return ap.parse_args()
+
+
+def copy_calibration():
+    """A plain copy of known size: 3 x 1 GiB read + 1 GiB written.  Under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE its per-dispatch figures give the
+    factors that turn the counters into bytes."""
+    import torch
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "dispatches": 3}))
+
+
+def read_traffic(path: str, kernel: str):
+    """HBM bytes per launch of `kernel` from a traffic summary: lines
+    `factor fetch F write W` and `<kernel> fetch_kib K write_kib K`
+    (rocprofv3 per-dispatch FETCH_SIZE / WRITE_SIZE averages)."""
+    if not os.path.exists(path):
+        return None
+    ff = fw = None
+    row = None
+    for line in open(path):
+        t = line.split()
+        if len(t) >= 5 and t[0] == "factor" and t[1] == "fetch" and t[3] == "write":
+            ff, fw = float(t[2]), float(t[4])
+        elif len(t) >= 5 and t[0] == kernel and t[1] == "fetch_kib" and t[3] == "write_kib":
+            row = float(t[2]), float(t[4])
+    if ff is None or row is None:
+        return None
+    return int(round((row[0] * ff + row[1] * fw) * 1024))
 
 
 def cpu_baseline(d, budget_s: float) -> dict:
@@ -69,6 +107,9 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import numpy as np
     import torch
 
@@ -122,6 +163,8 @@ def main():
         2 * pairs * D
     mlp1_gbs = mlp1_bytes / (kms["mlp1"] * 1e-3) / 1e9
     tok_s = c.tokens / (ms * 1e-3)
+    traffic = read_traffic(args.traffic or os.path.join(ROOT, "profiles", f"hbm_traffic_{c.name}.txt"),
+                           "mlp1")
     res = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -140,7 +183,7 @@ def main():
                    "weight_copies_rotated": copies},
         "roofline": {"bound": "hbm", "kernel": "grouped_gemm_kernel<mlp1>",
                      "achieved": round(mlp1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": mlp1_bytes,
                      "avg_launch_ms": round(kms["mlp1"], 5)},
         "layer": {"algorithmic_bytes": alg_bytes, "hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1),

@@ -1,10 +1,11 @@
 // gptoss_moe.hip — MI355X (gfx950) MXFP4 mixture-of-experts layer.
 //
 // Kernels (one stream, no host round trip):
-//   router_kernel  router GEMM in a pinned fp32 order (bit-reproducible).
-//   topk_kernel    top-k/softmax + expert histogram; the last workgroup
-//                  scans the histogram and writes the per-expert tile list.
-//   index_kernel   per-expert ballot compaction: compact row -> token map.
+//   route_kernel   router GEMM in a pinned fp32 order (bit-reproducible)
+//                  fused with top-k/softmax; per-block expert histogram.
+//   plan_kernel    counts, offsets, per-block row bases, tile list.
+//   index_gather_kernel  compact row -> token map; x rows gathered into
+//                  compact order.
 //   mlp1_kernel    grouped GEMM x[token(row)] . W1[e]^T, MXFP4 dequantised
 //                  in registers (v_cvt_scalef32_pk_bf16_fp4) into bf16 MFMA
 //                  operands; epilogue: bias + clamped SwiGLU on the
@@ -31,7 +32,10 @@ typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;  // register-friendl
 constexpr int kWave = 64;
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 8;
-constexpr int kMaxHidden = 4096;    // router keeps x rows in registers
+constexpr int kBlockTokensMin = 64;          // tokens per routing histogram block (at least)
+constexpr int kMaxBlocks = 64;               // histogram blocks per call (at most)
+constexpr int kHistCols = kMaxExperts + 1;   // experts + dropped slots
+constexpr int kMaxHidden = 4096;    // router stages x rows in LDS; GEMM scale blocks
 constexpr int kTileRows = 32;       // rows per grouped-GEMM tile (2 x 16)
 constexpr int kBlockN = 128;        // weight rows per workgroup (4 waves x 32)
 constexpr int kChunkK = 256;        // k per LDS chunk of activations
@@ -68,19 +72,15 @@ __device__ __forceinline__ uint32_t zero_scale_fix(uint32_t q, uint32_t e) {
 
 // ------------------------------------------------------- workspace map --
 struct WsLayout {
-    size_t hdr, counts_hot, counts, offsets, tiles, logits, topk_i, topk_w, local_ids, row_token,
-        row_w, row_slot, xg, act, slots, total;
+    size_t hdr, hist, blkbase, counts, offsets, tiles, logits, topk_i, topk_w, slot_e, local_ids,
+        row_token, row_w, row_slot, xg, act, slots, total;
     int max_tiles;
 };
 
-// hdr ints: DONE = workgroups finished (reset by the last one), NTILES = tile
-// count, STATUS_HOT = dropped slots of the running call, STATUS = last call's.
+// hdr ints: NTILES = tile count, STATUS = dropped slots of the last call.
 // XSTART / XCOUNT: the tile list is grouped by XCD; tiles of XCD x are
 // tiles[XSTART + x] .. + [XCOUNT + x].
-enum {
-    HDR_DONE = 0, HDR_NTILES = 1, HDR_STATUS_HOT = 2, HDR_STATUS = 4, HDR_XSTART = 8,
-    HDR_XCOUNT = 16, HDR_INTS = 256
-};
+enum { HDR_NTILES = 1, HDR_STATUS = 4, HDR_XSTART = 8, HDR_XCOUNT = 16, HDR_INTS = 256 };
 // Diagnostic builds (-DGPTOSS_TRACE) accumulate per-role cycle counts into the
 // header bytes 512..1023 (64 x u64); the product build compiles this away.
 #ifdef GPTOSS_TRACE
@@ -106,13 +106,15 @@ WsLayout ws_layout(const gptoss_moe_shape &s, int max_tokens) {
         return at;
     };
     L.hdr = take(HDR_INTS * 4);
-    L.counts_hot = take(E * 4);
+    L.hist = take((size_t)kMaxBlocks * kHistCols * 4);
+    L.blkbase = take((size_t)kMaxBlocks * E * 4);
     L.counts = take(E * 4);
     L.offsets = take((E + 1) * 4);
     L.tiles = take((size_t)L.max_tiles * 16);
     L.logits = take(T * E * 2);
     L.topk_i = take(P * 4);
     L.topk_w = take(P * 2);
+    L.slot_e = take(P * 4);
     L.local_ids = take(P * 4);
     L.row_token = take(P * 4);
     L.row_w = take(P * 4);
@@ -139,207 +141,160 @@ __device__ __forceinline__ bool better_pick(float av, int ai, float bv, int bi) 
     return false;
 }
 
+// Routing is three kernels with no synchronisation between workgroups inside
+// any of them (on a multi-XCD part a device-scope fence writes back and
+// invalidates the XCD's L2, which costs more than a kernel boundary):
+//   route_kernel         router logits + top-k/softmax for TB tokens per
+//                        workgroup, and a per-block expert histogram;
+//   plan_kernel          one workgroup: counts, offsets, per-block row bases,
+//                        the tile list; clears the histogram for the next call;
+//   index_gather_kernel  compact row map (ascending token order per expert)
+//                        and the gather of x rows into compact order.
+// Histogram blocks are runs of block_tokens tokens (a multiple of 64, at most
+// kMaxBlocks blocks per call); column E counts dropped slots.
+
+int hist_block_tokens(int T) {
+    const int per = kBlockTokensMin * kMaxBlocks;
+    return kBlockTokensMin * ((T + per - 1) / per);
+}
+
 // Router logits: logits[t][e] = bf16(x[t] . wr[e]) in fp32, no bias
 // (matmul_vec128_singlebuf_Abf16, matmul.hpp:1344, called at
 // getp_run.cpp:2612-2620).  The fp32 order is pinned so the CPU oracle can
 // reproduce every logit bit for bit: 16 partial sums p[l] (l = 0..15), each
 // an fmaf chain over k = 128 i + 8 l + j (i ascending, then j = 0..7), then
-// p[l] += p[l ^ s] for s = 8, 4, 2, 1.  A 16-lane group computes TT tokens x
-// EE experts of such dot products (lane l owns partial l of all of them), so
-// each loaded bf16 is converted once and used TT or EE times.
-template <int TT, int EE>
-__global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict__ x,
-                                                    const uint16_t *__restrict__ wr, int T, int H,
-                                                    int E, uint16_t *__restrict__ logits) {
-    const int lane16 = threadIdx.x & 15;
-    const int grp = blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int n_eb = (E + EE - 1) / EE;
-    const int eb = grp % n_eb, tb = grp / n_eb;
-    if (tb * TT >= T) return;  // whole 16-lane group idle (no shuffles follow for it)
-    const uint16_t *xp[TT];
-    const uint16_t *wp[EE];
-#pragma unroll
-    for (int i = 0; i < TT; ++i) xp[i] = x + (size_t)min(tb * TT + i, T - 1) * H;
-#pragma unroll
-    for (int i = 0; i < EE; ++i) wp[i] = wr + (size_t)min(eb * EE + i, E - 1) * H;
-    float acc[TT][EE];
-#pragma unroll
-    for (int i = 0; i < TT; ++i)
-#pragma unroll
-        for (int j = 0; j < EE; ++j) acc[i][j] = 0.f;
-    // NB iterations' loads are issued before any of them is used
-    constexpr int NB = (TT + EE) <= 2 ? 4 : (TT + EE) <= 6 ? 2 : 1;
-    const int NI = (H + 127) / 128;
-    for (int it0 = 0; it0 < NI; it0 += NB) {
-        uint4 xv[NB][TT], wv[NB][EE];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int k = min(128 * (it0 + b) + 8 * lane16, H - 8);
-#pragma unroll
-            for (int i = 0; i < TT; ++i) xv[b][i] = *reinterpret_cast<const uint4 *>(xp[i] + k);
-#pragma unroll
-            for (int i = 0; i < EE; ++i) wv[b][i] = *reinterpret_cast<const uint4 *>(wp[i] + k);
-        }
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (128 * (it0 + b) + 8 * lane16 >= H) break;  // no partial of this lane left
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float xl[TT], xh[TT];
-#pragma unroll
-                for (int i = 0; i < TT; ++i) {
-                    const uint4 v = xv[b][i];
-                    const uint32_t d = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
-                    xl[i] = __uint_as_float(d << 16);
-                    xh[i] = __uint_as_float(d & 0xffff0000u);
-                }
-#pragma unroll
-                for (int j = 0; j < EE; ++j) {
-                    const uint4 v = wv[b][j];
-                    const uint32_t d = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
-                    const float wl = __uint_as_float(d << 16), wh = __uint_as_float(d & 0xffff0000u);
-#pragma unroll
-                    for (int i = 0; i < TT; ++i) {
-                        acc[i][j] = __builtin_fmaf(xl[i], wl, acc[i][j]);
-                        acc[i][j] = __builtin_fmaf(xh[i], wh, acc[i][j]);
-                    }
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < TT; ++i)
-#pragma unroll
-        for (int j = 0; j < EE; ++j) {
-            float v = acc[i][j];
-#pragma unroll
-            for (int st = 8; st >= 1; st >>= 1) v = __fadd_rn(v, __shfl_xor(v, st, 16));
-            const int t = tb * TT + i, e = eb * EE + j;
-            if (lane16 == 0 && t < T && e < E) logits[(size_t)t * E + e] = f2bf(v);
-        }
-}
-
-// Wave-inclusive scan of v over 64 lanes.
-__device__ __forceinline__ int wave_scan(int v, int lane) {
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const int o = __shfl_up(v, s, 64);
-        if (lane >= s) v += o;
-    }
-    return v;
-}
-
-// Number of r in [0, n) with r % 8 == x.
-__device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x) / 8 + 1 : 0; }
-
-// One wave: read-and-reset the histogram, write counts and exclusive offsets,
-// and the tile list (kTileRows rows per tile) grouped by XCD.  An expert's
-// tiles are cut into units of up to 2 tiles; the U2 2-tile units are dealt
-// to the 8 XCDs round robin (unit rank r goes to XCD r % 8), then the U1
-// 1-tile units continue the deal.  That balances tiles per XCD within 2,
-// and both tiles of a unit share one XCD's L2 (the GEMM streams the unit's
-// weights once for both).  Tiles of XCD x occupy
-// tiles[xstart(x) .. xstart(x) + xcount(x)), 2-tile units first.
-__device__ void build_tiles(int32_t *counts_hot, int32_t *__restrict__ counts,
-                            int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr,
-                            int E, int lane) {
-    // lane l owns experts 4l .. 4l+3
-    int c[4], nt[4], n2[4], n1[4];
-    int csum = 0, s2 = 0, s1 = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = 4 * lane + j;
-        c[j] = e < E ? atomicExch(&counts_hot[e], 0) : 0;
-        nt[j] = (c[j] + kTileRows - 1) / kTileRows;
-        n2[j] = nt[j] / 2;
-        n1[j] = nt[j] % 2;
-        csum += c[j];
-        s2 += n2[j];
-        s1 += n1[j];
-    }
-    const int cinc = wave_scan(csum, lane), i2 = wave_scan(s2, lane), i1 = wave_scan(s1, lane);
-    const int U2 = __shfl(i2, 63, 64), U1 = __shfl(i1, 63, 64);
-    auto xcount = [&](int x) { return 2 * n_mod8(U2, x) + n_mod8(U2 + U1, x) - n_mod8(U2, x); };
-    int xstart[8];
-    {
-        int acc = 0;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            xstart[x] = acc;
-            acc += xcount(x);
-        }
-    }
-    int off = cinc - csum, r2 = i2 - s2, r1 = i1 - s1;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = 4 * lane + j;
-        if (e < E) {
-            counts[e] = c[j];
-            offsets[e] = off;
-            for (int m = 0; m < nt[j]; ++m) {
-                const int u = m / 2;
-                int x, pos;  // XCD of the unit and the tile's position in that XCD
-                if (u < n2[j]) {
-                    const int rank = r2 + u;
-                    x = rank & 7;
-                    pos = 2 * (rank / 8) + (m & 1);
-                } else {
-                    const int rank = U2 + r1;
-                    x = rank & 7;
-                    pos = 2 * n_mod8(U2, x) + n_mod8(rank, x) - n_mod8(U2, x);
-                }
-                int base = 0;
-#pragma unroll
-                for (int xx = 0; xx < 8; ++xx)
-                    if (xx == x) base = xstart[xx];
-                Tile tl;
-                tl.expert = e;
-                tl.row0 = off + m * kTileRows;
-                tl.rows = min(kTileRows, c[j] - m * kTileRows);
-                tl.pad = 0;
-                tiles[base + pos] = tl;
-            }
-        }
-        off += c[j];
-        r2 += n2[j];
-        r1 += n1[j];
-    }
-    if (lane == 63) {
-        offsets[E] = off;
-        hdr[HDR_NTILES] = 2 * U2 + U1;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            hdr[HDR_XSTART + x] = xstart[x];
-            hdr[HDR_XCOUNT + x] = xcount(x);
-        }
-        hdr[HDR_STATUS] = atomicExch(&hdr[HDR_STATUS_HOT], 0);
-        hdr[HDR_DONE] = 0;
-    }
-}
-
-constexpr int kTopkTokens = 4;  // one wave per token
-
-// Top-k + softmax (route_select_softmax_kernel_bf16io, moe.hpp:465-599) for
-// one token per wave: scores fp32 = logit + bias; K rounds of the reference's
+// p[l] += p[l ^ s] for s = 8, 4, 2, 1.  The workgroup's TB x rows sit in LDS;
+// 16-lane group g owns experts g EE .. g EE + EE - 1 for all TB tokens (lane
+// l holds partial l of each), streaming its router rows through a register
+// ring kD steps deep.  LDS keeps the bf16-rounded logits for the top-k.
+//
+// Top-k + softmax (route_select_softmax_kernel_bf16io, moe.hpp:465-599), one
+// wave per token: scores fp32 = logit + bias; K rounds of the reference's
 // arg-max, a halving tree over clamp(nextpow2(E), 64, 512) threads, emulated
 // exactly with 64 lanes x R slots (slot r of lane l = thread l + 64 r); then
-// softmax over the K selected.  Counts live slots per expert with device
-// atomics; the last workgroup to finish scans the histogram (resetting it)
-// into counts, offsets and the tile list.  With forced routing the given
-// indices and weights are copied and validated instead.
-__global__ __launch_bounds__(256) void topk_kernel(
-    const uint16_t *__restrict__ logits, const uint16_t *__restrict__ br,
-    const int32_t *__restrict__ forced_i, const uint16_t *__restrict__ forced_w, int T, int E,
-    int K, int32_t *__restrict__ topk_i, uint16_t *__restrict__ topk_w,
-    int32_t *__restrict__ local_ids, int32_t *counts_hot, int32_t *__restrict__ counts,
-    int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr, int nthreads_ref) {
-    __shared__ int s_last;
+// softmax over the K selected.  With forced routing the given indices and
+// weights are validated and copied instead (invalid or repeated experts are
+// dropped).  slot_e[t][k] = expert of a live slot, -1 for a dropped one.
+template <int TB, int EE>
+__global__ __launch_bounds__(256) void route_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ wr,
+    const uint16_t *__restrict__ br, const int32_t *__restrict__ forced_i,
+    const uint16_t *__restrict__ forced_w, int T, int H, int E, int K, int nthreads_ref,
+    int block_tokens, uint16_t *__restrict__ logits, int32_t *__restrict__ topk_i,
+    uint16_t *__restrict__ topk_w, int32_t *__restrict__ slot_e, int32_t *__restrict__ hist) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[TB * kMaxHidden];
+    __shared__ float sc[TB][kMaxExperts];
+    __shared__ int shist[kHistCols];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = blockIdx.x * kTopkTokens + wave;
+    const int t0 = blockIdx.x * TB;
+    const int nt = min(TB, T - t0);
+    for (int c = tid; c <= E; c += 256) shist[c] = 0;
 
     if (forced_i == nullptr) {
-        if (t < T) {
-            const int R = nthreads_ref / 64;  // 1, 2 or 4 slots per lane
+        // ---- stage the x rows (rows past T repeat the last token); every
+        // load is issued before the first store
+        const int h8 = H / 8, n8 = TB * h8;
+        constexpr int NL = TB * (kMaxHidden / 8) / 256;
+        uint4 v[NL];
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = min(tid + 256 * u, n8 - 1);
+            const int r = i / h8, c = i - r * h8;
+            v[u] = *reinterpret_cast<const uint4 *>(x + (size_t)(t0 + min(r, nt - 1)) * H + 8 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = tid + 256 * u;
+            if (i < n8) *reinterpret_cast<uint4 *>(&xs[8 * i]) = v[u];
+        }
+        __syncthreads();
+
+        // ---- logits
+        const int l16 = tid & 15, grp = tid >> 4;
+        const uint16_t *wp[EE];
+#pragma unroll
+        for (int j = 0; j < EE; ++j) wp[j] = wr + (size_t)min(grp * EE + j, E - 1) * H;
+        constexpr int kD = EE >= 8 ? 2 : 16 / EE;
+        const int NI = (H + 127) / 128;
+        uint4 wv[kD][EE];
+        float acc[TB][EE];
+#pragma unroll
+        for (int i = 0; i < TB; ++i)
+#pragma unroll
+            for (int j = 0; j < EE; ++j) acc[i][j] = 0.f;
+        auto issue = [&](int i, int r) {
+            const int k = min(128 * min(i, NI - 1) + 8 * l16, H - 8);
+#pragma unroll
+            for (int j = 0; j < EE; ++j) wv[r][j] = *reinterpret_cast<const uint4 *>(wp[j] + k);
+        };
+        // issue order = use order (the waits count on it): the scheduler may
+        // not move loads across the barriers below
+#pragma unroll
+        for (int r = 0; r < kD; ++r) {
+            issue(r, r);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int i0 = 0; i0 < NI; i0 += kD) {
+#pragma unroll
+            for (int r = 0; r < kD; ++r) {
+                const int i = i0 + r;
+                __builtin_amdgcn_sched_barrier(0);
+                if (i < NI && 128 * i + 8 * l16 < H) {
+                    uint4 xv[TB];
+#pragma unroll
+                    for (int tt = 0; tt < TB; ++tt)
+                        xv[tt] = *reinterpret_cast<const uint4 *>(&xs[tt * H + 128 * i + 8 * l16]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        float xl[TB], xh[TB];
+#pragma unroll
+                        for (int tt = 0; tt < TB; ++tt) {
+                            const uint4 a = xv[tt];
+                            const uint32_t d = q == 0 ? a.x : q == 1 ? a.y : q == 2 ? a.z : a.w;
+                            xl[tt] = __uint_as_float(d << 16);
+                            xh[tt] = __uint_as_float(d & 0xffff0000u);
+                        }
+#pragma unroll
+                        for (int j = 0; j < EE; ++j) {
+                            const uint4 b = wv[r][j];
+                            const uint32_t d = q == 0 ? b.x : q == 1 ? b.y : q == 2 ? b.z : b.w;
+                            const float wl = __uint_as_float(d << 16);
+                            const float wh = __uint_as_float(d & 0xffff0000u);
+#pragma unroll
+                            for (int tt = 0; tt < TB; ++tt) {
+                                acc[tt][j] = __builtin_fmaf(xl[tt], wl, acc[tt][j]);
+                                acc[tt][j] = __builtin_fmaf(xh[tt], wh, acc[tt][j]);
+                            }
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                issue(i + kD, r);
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+            for (int j = 0; j < EE; ++j) {
+                float s = acc[tt][j];
+#pragma unroll
+                for (int st = 8; st >= 1; st >>= 1) s = __fadd_rn(s, __shfl_xor(s, st, 16));
+                const int e = grp * EE + j;
+                if (l16 == 0 && e < E && tt < nt) {
+                    const uint16_t b = f2bf(s);
+                    logits[(size_t)(t0 + tt) * E + e] = b;
+                    sc[tt][e] = bf2f(b);
+                }
+            }
+        __syncthreads();
+
+        // ---- top-k + softmax, one wave per token
+        const int R = nthreads_ref / 64;  // 1, 2 or 4 slots per lane
+        float bias[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bias[r] = bf2f(br[min(lane + 64 * r, E - 1)]);
+        for (int tt = wave; tt < nt; tt += 4) {
+            const int t = t0 + tt;
             float sv[4];
             int si[4];
             uint32_t visited = 0;
@@ -347,7 +302,7 @@ __global__ __launch_bounds__(256) void topk_kernel(
             for (int r = 0; r < 4; ++r) {
                 const int i = lane + 64 * r;
                 const bool ok = r < R && i < E;
-                sv[r] = ok ? __fadd_rn(bf2f(logits[(size_t)t * E + i]), bf2f(br[i])) : -INFINITY;
+                sv[r] = ok ? __fadd_rn(sc[tt][i], bias[r]) : -INFINITY;
                 si[r] = ok ? i : E;
             }
             int sel_i[kMaxTopK];
@@ -411,110 +366,257 @@ __global__ __launch_bounds__(256) void topk_kernel(
                     const int e = sel_i[s] < E ? sel_i[s] : -1;
                     topk_i[(size_t)t * K + s] = e;
                     topk_w[(size_t)t * K + s] = f2bf(__fmul_rn(ex[s], inv));
-                    if (e >= 0) {
-                        atomicAdd(&counts_hot[e], 1);
-                    } else {
-                        local_ids[(size_t)t * K + s] = -1;
-                        atomicAdd(&hdr[HDR_STATUS_HOT], 1);
-                    }
+                    slot_e[(size_t)t * K + s] = e;
+                    atomicAdd(&shist[e >= 0 ? e : E], 1);
                 }
             }
         }
     } else {
-        if (tid < kTopkTokens * K) {
-            const int tt = blockIdx.x * kTopkTokens + tid / K, s = tid % K;
-            if (tt < T) {
-                const int e = forced_i[(size_t)tt * K + s];
+        __syncthreads();  // shist cleared
+        if (tid < TB * K) {
+            const int tt = tid / K, s = tid - tt * K;
+            if (tt < nt) {
+                const size_t t = (size_t)(t0 + tt);
+                const int e = forced_i[t * K + s];
                 bool live = e >= 0 && e < E;
                 for (int j = 0; j < s; ++j)
-                    if (forced_i[(size_t)tt * K + j] == e) live = false;
-                topk_i[(size_t)tt * K + s] = e;
-                topk_w[(size_t)tt * K + s] = forced_w[(size_t)tt * K + s];
-                if (live) {
-                    atomicAdd(&counts_hot[e], 1);
-                } else {
-                    local_ids[(size_t)tt * K + s] = -1;
-                    atomicAdd(&hdr[HDR_STATUS_HOT], 1);
-                }
+                    if (forced_i[t * K + j] == e) live = false;
+                topk_i[t * K + s] = e;
+                topk_w[t * K + s] = forced_w[t * K + s];
+                slot_e[t * K + s] = live ? e : -1;
+                atomicAdd(&shist[live ? e : E], 1);
             }
         }
     }
-
-    // ---- last workgroup: scan, reset histogram, tile list
-    __threadfence();
     __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&hdr[HDR_DONE], 1) == (int)gridDim.x - 1);
-    __syncthreads();
-    if (!s_last || wave != 0) return;
-    __threadfence();
-    build_tiles(counts_hot, counts, offsets, tiles, hdr, E, lane);
+    int32_t *hrow = hist + (size_t)(t0 / block_tokens) * kHistCols;
+    for (int c = tid; c <= E; c += 256)
+        if (shist[c]) atomicAdd(&hrow[c], shist[c]);
 }
 
-// Compact row map (route_build_index_kernel_bf16wts, moe.hpp:1173-1270): one
-// workgroup per expert; rows of expert e are assigned in ascending token
-// order with wave ballots.
-__global__ __launch_bounds__(256) void index_kernel(const int32_t *__restrict__ topk_i,
-                                                   const uint16_t *__restrict__ topk_w, int T, int K,
-                                                   int E, int H, const int32_t *__restrict__ offsets,
-                                                   const uint16_t *__restrict__ x,
-                                                   int32_t *__restrict__ local_ids,
-                                                   int32_t *__restrict__ row_token,
-                                                   float *__restrict__ row_w,
-                                                   int32_t *__restrict__ row_slot,
-                                                   uint16_t *__restrict__ xg) {
-    __shared__ int s_wcount[4];
-    const int e = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int carry = 0;
-    const int base_row = offsets[e];
-    for (int base = 0; base < T; base += 256) {
-        const int t = base + tid;
-        int kk = -1;
-        if (t < T) {
-            for (int s = 0; s < K; ++s) {
-                const int v = topk_i[(size_t)t * K + s];
-                if (v == e) {
-                    kk = s;
-                    break;
-                }
-            }
-        }
-        const uint64_t m = __ballot(kk >= 0);
-        const int rank = __popcll(m & ((1ull << lane) - 1ull));
-        if (lane == 0) s_wcount[wave] = __popcll(m);
-        __syncthreads();
-        int wbase = 0, total = 0;
+// Wave-inclusive scan of v over 64 lanes.
+__device__ __forceinline__ int wave_scan(int v, int lane) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            if (w < wave) wbase += s_wcount[w];
-            total += s_wcount[w];
+    for (int s = 1; s < 64; s <<= 1) {
+        const int o = __shfl_up(v, s, 64);
+        if (lane >= s) v += o;
+    }
+    return v;
+}
+
+// Number of r in [0, n) with r % 8 == x.
+__device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x) / 8 + 1 : 0; }
+
+// One wave: from the per-expert totals tot[0..E) (and dropped slots tot[E]),
+// write counts, exclusive offsets (global and offs[] in LDS) and the tile list
+// (kTileRows rows per tile) grouped by XCD.  An expert's tiles are cut into
+// units of up to 2 tiles; the U2 2-tile units are dealt to the 8 XCDs round
+// robin (unit rank r goes to XCD r % 8), then the U1 1-tile units continue the
+// deal.  That balances tiles per XCD within 2, and both tiles of a unit share
+// one XCD's L2 (the GEMM streams the unit's weights once for both).  Tiles of
+// XCD x occupy tiles[xstart(x) .. xstart(x) + xcount(x)), 2-tile units first.
+__device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ counts,
+                            int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr,
+                            int E, int lane) {
+    // lane l owns experts 4l .. 4l+3
+    int c[4], nt[4], n2[4], n1[4];
+    int csum = 0, s2 = 0, s1 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        c[j] = e < E ? tot[e] : 0;
+        nt[j] = (c[j] + kTileRows - 1) / kTileRows;
+        n2[j] = nt[j] / 2;
+        n1[j] = nt[j] % 2;
+        csum += c[j];
+        s2 += n2[j];
+        s1 += n1[j];
+    }
+    const int cinc = wave_scan(csum, lane), i2 = wave_scan(s2, lane), i1 = wave_scan(s1, lane);
+    const int U2 = __shfl(i2, 63, 64), U1 = __shfl(i1, 63, 64);
+    auto xcount = [&](int x) { return 2 * n_mod8(U2, x) + n_mod8(U2 + U1, x) - n_mod8(U2, x); };
+    int xstart[8];
+    {
+        int acc = 0;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            xstart[x] = acc;
+            acc += xcount(x);
         }
-        if (kk >= 0) {
-            const int local = wbase + rank;
-            const int row = base_row + carry + local;
-            local_ids[(size_t)t * K + kk] = row;
-            row_token[row] = t;
-            row_w[row] = bf2f(topk_w[(size_t)t * K + kk]);
-            row_slot[row] = t * K + kk;
+    }
+    int off = cinc - csum, r2 = i2 - s2, r1 = i1 - s1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        if (e < E) {
+            counts[e] = c[j];
+            offsets[e] = off;
+            offs[e] = off;
+            for (int m = 0; m < nt[j]; ++m) {
+                const int u = m / 2;
+                int x, pos;  // XCD of the unit and the tile's position in that XCD
+                if (u < n2[j]) {
+                    const int rank = r2 + u;
+                    x = rank & 7;
+                    pos = 2 * (rank / 8) + (m & 1);
+                } else {
+                    const int rank = U2 + r1;
+                    x = rank & 7;
+                    pos = 2 * n_mod8(U2, x) + n_mod8(rank, x) - n_mod8(U2, x);
+                }
+                int base = 0;
+#pragma unroll
+                for (int xx = 0; xx < 8; ++xx)
+                    if (xx == x) base = xstart[xx];
+                Tile tl;
+                tl.expert = e;
+                tl.row0 = off + m * kTileRows;
+                tl.rows = min(kTileRows, c[j] - m * kTileRows);
+                tl.pad = 0;
+                tiles[base + pos] = tl;
+            }
         }
-        carry += total;
-        __syncthreads();
+        off += c[j];
+        r2 += n2[j];
+        r1 += n1[j];
+    }
+    if (lane == 63) {
+        offsets[E] = off;
+        offs[E] = off;
+        hdr[HDR_NTILES] = 2 * U2 + U1;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            hdr[HDR_XSTART + x] = xstart[x];
+            hdr[HDR_XCOUNT + x] = xcount(x);
+        }
+        hdr[HDR_STATUS] = tot[E];
     }
 }
 
-// Gather (pack_rows_kernel_bf16_in, moe.hpp:983-1048): xg[row] = x[token(row)]
-// for the compact rows; workgroups stride over rows, 16 bytes per thread.
-__global__ __launch_bounds__(256) void gather_kernel(const uint16_t *__restrict__ x,
-                                                    const int32_t *__restrict__ row_token,
-                                                    const int32_t *__restrict__ offsets, int E,
-                                                    int H, uint16_t *__restrict__ xg) {
-    const int P = offsets[E];
+// Plan (the scan half of route_build_index_kernel_bf16wts, moe.hpp:1173-1270),
+// one workgroup: reads and clears the block histogram, column-scans it into
+// per-block row bases blkbase[b][e] = offsets[e] + rows of e in blocks < b,
+// and builds counts, offsets and the tile list.
+__global__ __launch_bounds__(1024) void plan_kernel(int32_t *__restrict__ hist, int n_blk, int E,
+                                                   int32_t *__restrict__ counts,
+                                                   int32_t *__restrict__ offsets,
+                                                   int32_t *__restrict__ blkbase,
+                                                   Tile *__restrict__ tiles, int32_t *hdr) {
+    __shared__ int h[kMaxBlocks * kHistCols];
+    __shared__ int tot[kHistCols];
+    __shared__ int offs[kMaxExperts + 1];
+    const int tid = threadIdx.x;
+    const int n = n_blk * kHistCols;
+    constexpr int NL = (kMaxBlocks * kHistCols + 1023) / 1024;
+    int v[NL];
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+        const int i = tid + 1024 * u;
+        v[u] = i < n ? hist[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+        const int i = tid + 1024 * u;
+        if (i < n) {
+            h[i] = v[u];
+            hist[i] = 0;
+        }
+    }
+    __syncthreads();
+    if (tid <= E) {  // exclusive scan of column tid over the blocks
+        int s = 0;
+        for (int b = 0; b < n_blk; ++b) {
+            const int c = h[b * kHistCols + tid];
+            h[b * kHistCols + tid] = s;
+            s += c;
+        }
+        tot[tid] = s;
+    }
+    __syncthreads();
+    if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tid);
+    __syncthreads();
+    for (int i = tid; i < n_blk * E; i += 1024) {
+        const int b = i / E, e = i - b * E;
+        blkbase[i] = offs[e] + h[b * kHistCols + e];
+    }
+}
+
+// Compact row map (route_build_index_kernel_bf16wts, moe.hpp:1173-1270) and
+// gather (pack_rows_kernel_bf16_in, moe.hpp:983-1048).  Workgroup (g, b)
+// walks block b's slots in rounds of 256 (slot t*K + k ascending, so rows of
+// an expert come in ascending token order): in-wave rank by shuffles, wave
+// counts in LDS, running per-expert row counters.  Workgroup g = 0 writes the
+// row map; every workgroup copies the x rows of the round's slots j with
+// j % G == g into xg[row].
+__global__ __launch_bounds__(256) void index_gather_kernel(
+    const int32_t *__restrict__ slot_e, const uint16_t *__restrict__ topk_w,
+    const int32_t *__restrict__ blkbase, const uint16_t *__restrict__ x, int T, int K, int E,
+    int H, int block_tokens, int32_t *__restrict__ local_ids, int32_t *__restrict__ row_token,
+    float *__restrict__ row_w, int32_t *__restrict__ row_slot, uint16_t *__restrict__ xg) {
+    __shared__ int run[kMaxExperts];
+    __shared__ int wcnt[4][kMaxExperts];
+    __shared__ int srow[256], stok[256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = blockIdx.x, G = gridDim.x, b = blockIdx.y;
+    const int t0 = b * block_tokens;
+    const int nslots = min(block_tokens, T - t0) * K;
+    const int s0 = t0 * K;
     const int h8 = H / 8;
-    const size_t n = (size_t)P * h8;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const int r = (int)(i / h8), c = (int)(i - (size_t)r * h8);
-        *reinterpret_cast<uint4 *>(xg + (size_t)r * H + 8 * c) =
-            *reinterpret_cast<const uint4 *>(x + (size_t)row_token[r] * H + 8 * c);
+    for (int e = tid; e < E; e += 256) run[e] = blkbase[b * E + e];
+    for (int r0 = 0; r0 < nslots; r0 += 256) {
+        for (int e = tid; e < E; e += 256) wcnt[0][e] = wcnt[1][e] = wcnt[2][e] = wcnt[3][e] = 0;
+        __syncthreads();
+        const int s = r0 + tid;
+        const int e = s < nslots ? slot_e[s0 + s] : -1;
+        int rank = 0, same = 0;
+        for (int j = 0; j < 64; ++j) {
+            const int ej = __shfl(e, j, 64);
+            if (ej == e) {
+                ++same;
+                if (j < lane) ++rank;
+            }
+        }
+        if (e >= 0 && rank == same - 1) wcnt[wave][e] = same;
+        __syncthreads();
+        int row = -1;
+        if (e >= 0) {
+            row = run[e] + rank;
+            for (int w = 0; w < wave; ++w) row += wcnt[w][e];
+        }
+        srow[tid] = row;
+        stok[tid] = (s0 + s) / K;
+        if (g == 0 && s < nslots) local_ids[s0 + s] = row;  // -1 for a dropped slot
+        if (g == 0 && e >= 0) {
+            const int t = (s0 + s) / K;
+            row_token[row] = t;
+            row_w[row] = bf2f(topk_w[s0 + s]);
+            row_slot[row] = s0 + s;
+        }
+        __syncthreads();
+        for (int e2 = tid; e2 < E; e2 += 256)
+            run[e2] += wcnt[0][e2] + wcnt[1][e2] + wcnt[2][e2] + wcnt[3][e2];
+        // gather, 4 loads in flight per thread
+        const int cnt = min(256, nslots - r0);
+        const int mine = cnt > g ? (cnt - g + G - 1) / G : 0;
+        const int n = mine * h8;
+        for (int i0 = tid; i0 < n; i0 += 4 * 256) {
+            uint4 v[4];
+            int dst[4], col[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = min(i0 + 256 * u, n - 1);
+                const int m = i / h8, c = i - m * h8;
+                const int j = g + G * m;
+                dst[u] = srow[j];
+                col[u] = 8 * c;
+                v[u] = *reinterpret_cast<const uint4 *>(x + (size_t)stok[j] * H + 8 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + 256 * u < n && dst[u] >= 0)
+                    *reinterpret_cast<uint4 *>(xg + (size_t)dst[u] * H + col[u]) = v[u];
+        }
+        __syncthreads();
     }
 }
 
@@ -1127,7 +1229,7 @@ bool shape_ok(const gptoss_moe_shape *s) {
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 struct Ptrs {
-    int32_t *hdr, *counts_hot, *counts, *offsets, *topk_i, *local_ids, *row_token;
+    int32_t *hdr, *hist, *blkbase, *counts, *offsets, *topk_i, *slot_e, *local_ids, *row_token;
     Tile *tiles;
     uint16_t *logits, *topk_w, *act, *slots, *xg;
     int32_t *row_slot;
@@ -1138,7 +1240,9 @@ Ptrs ws_ptrs(const WsLayout &L, void *ws) {
     char *b = (char *)ws;
     Ptrs p;
     p.hdr = (int32_t *)(b + L.hdr);
-    p.counts_hot = (int32_t *)(b + L.counts_hot);
+    p.hist = (int32_t *)(b + L.hist);
+    p.blkbase = (int32_t *)(b + L.blkbase);
+    p.slot_e = (int32_t *)(b + L.slot_e);
     p.counts = (int32_t *)(b + L.counts);
     p.offsets = (int32_t *)(b + L.offsets);
     p.tiles = (Tile *)(b + L.tiles);
@@ -1179,45 +1283,59 @@ struct Marks {
     }
 };
 
+template <int TB, int EE>
+void launch_route_kernel(const gptoss_moe_shape *s, const gptoss_moe_weights *w,
+                         const uint16_t *x, int T, const int32_t *fi, const uint16_t *fw,
+                         int nthreads_ref, int bt, const Ptrs &p, hipStream_t st) {
+    hipLaunchKernelGGL((route_kernel<TB, EE>), dim3((T + TB - 1) / TB), dim3(256), 0, st, x,
+                       w->router_w, w->router_b, fi, fw, T, s->hidden, s->n_experts, s->top_k,
+                       nthreads_ref, bt, p.logits, p.topk_i, p.topk_w, p.slot_e, p.hist);
+}
+
+template <int TB>
+void launch_route_tb(int ee, const gptoss_moe_shape *s, const gptoss_moe_weights *w,
+                     const uint16_t *x, int T, const int32_t *fi, const uint16_t *fw,
+                     int nthreads_ref, int bt, const Ptrs &p, hipStream_t st) {
+    switch (ee) {
+    case 1: launch_route_kernel<TB, 1>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
+    case 2: launch_route_kernel<TB, 2>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
+    case 4: launch_route_kernel<TB, 4>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
+    case 8: launch_route_kernel<TB, 8>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
+    default: launch_route_kernel<TB, (TB > 4 ? 8 : 16)>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+    }
+}
+
 int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                  int T, const int32_t *fi, const uint16_t *fw, const Ptrs &p, hipStream_t st,
                  Marks *mk = nullptr) {
     int nthreads_ref = 1;
     while (nthreads_ref < s->n_experts) nthreads_ref <<= 1;
     nthreads_ref = nthreads_ref < 64 ? 64 : (nthreads_ref > 512 ? 512 : nthreads_ref);
-    const int H = s->hidden, E = s->n_experts;
-    if (fi == nullptr) {
-        // register tile per 16-lane group: the largest that still gives >= 2048 waves
-        auto groups = [&](int tt, int ee) { return (long)((T + tt - 1) / tt) * ((E + ee - 1) / ee); };
-        auto blocks = [&](long g) { return dim3((unsigned)((g + 15) / 16)); };
-        if (groups(4, 8) >= 8192)
-            hipLaunchKernelGGL((router_kernel<4, 8>), blocks(groups(4, 8)), dim3(256), 0, st, x,
-                               w->router_w, T, H, E, p.logits);
-        else if (groups(2, 4) >= 8192)
-            hipLaunchKernelGGL((router_kernel<2, 4>), blocks(groups(2, 4)), dim3(256), 0, st, x,
-                               w->router_w, T, H, E, p.logits);
-        else if (groups(2, 2) >= 8192)
-            hipLaunchKernelGGL((router_kernel<2, 2>), blocks(groups(2, 2)), dim3(256), 0, st, x,
-                               w->router_w, T, H, E, p.logits);
-        else
-            hipLaunchKernelGGL((router_kernel<1, 1>), blocks(groups(1, 1)), dim3(256), 0, st, x,
-                               w->router_w, T, H, E, p.logits);
-    }
-    hipLaunchKernelGGL(topk_kernel, dim3((T + kTopkTokens - 1) / kTopkTokens), dim3(256), 0, st,
-                       p.logits, w->router_b, fi, fw, T, E, s->top_k, p.topk_i, p.topk_w,
-                       p.local_ids, p.counts_hot, p.counts, p.offsets, p.tiles, p.hdr,
-                       nthreads_ref);
+    const int E = s->n_experts;
+    const int bt = hist_block_tokens(T);
+    const int n_blk = (T + bt - 1) / bt;
+    // tokens per route workgroup: enough workgroups to cover the CUs at small
+    // T, more router-row reuse at large T; experts per 16-lane group: E / 16
+    int tb = T >= 2048 ? 8 : T >= 1024 ? 4 : 1;
+    const int ee = E <= 16 ? 1 : E <= 32 ? 2 : E <= 64 ? 4 : E <= 128 ? 8 : 16;
+    if (ee == 16 && tb == 8) tb = 4;
+    if (fi != nullptr) tb = 8;  // no router GEMM
+    if (tb == 8 && fi != nullptr)
+        launch_route_kernel<8, 1>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+    else if (tb == 8)
+        launch_route_tb<8>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+    else if (tb == 4)
+        launch_route_tb<4>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+    else
+        launch_route_tb<1>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, p.hist, n_blk, E, p.counts,
+                       p.offsets, p.blkbase, p.tiles, p.hdr);
     if (mk) mk->mark(st);
-    hipLaunchKernelGGL(index_kernel, dim3(s->n_experts), dim3(256), 0, st, p.topk_i, p.topk_w, T,
-                       s->top_k, s->n_experts, s->hidden, p.offsets, x, p.local_ids, p.row_token,
+    int G = 8 * device_cus() / n_blk;
+    G = G < 1 ? 1 : (G > 256 ? 256 : G);
+    hipLaunchKernelGGL(index_gather_kernel, dim3(G, n_blk), dim3(256), 0, st, p.slot_e, p.topk_w,
+                       p.blkbase, x, T, s->top_k, E, s->hidden, bt, p.local_ids, p.row_token,
                        p.row_w, p.row_slot, p.xg);
-    {
-        long rows = (long)T * s->top_k;
-        long g = (rows * (s->hidden / 8) + 255) / 256;
-        if (g > 4L * device_cus()) g = 4L * device_cus();
-        hipLaunchKernelGGL(gather_kernel, dim3((unsigned)g), dim3(256), 0, st, x, p.row_token,
-                           p.offsets, s->n_experts, s->hidden, p.xg);
-    }
     if (mk) mk->mark(st);
     return hip_status(hipGetLastError());
 }
