@@ -690,15 +690,24 @@ struct ItemMap {
         xcd = (int)blockIdx.x & 7;
         w = (int)blockIdx.x >> 3;
         Gx = (int)gridDim.x >> 3;
-        base = hdr[HDR_XSTART + xcd];
-        ntx = hdr[HDR_XCOUNT + xcd];
+        typedef const __attribute__((address_space(4))) int32_t *ConstInts;
+        base = ((ConstInts)hdr)[HDR_XSTART + xcd];
+        ntx = ((ConstInts)hdr)[HDR_XCOUNT + xcd];
         const int items_x = ntx * nblk;
         n_items = items_x > w ? (items_x - w + Gx - 1) / Gx : 0;
     }
+    // The tile list is read through the constant address space: a scalar
+    // load (its wait does not drain the wave's vector loads), valid because
+    // no kernel that reads it writes it.
     __device__ __forceinline__ void at(const Tile *tiles, int i, Tile &tl, int &nb) const {
         const int ii = w + i * Gx;
         nb = ii / ntx;
-        tl = tiles[base + ii - nb * ntx];
+        typedef const __attribute__((address_space(4))) int32_t *ConstInts;
+        const ConstInts t = (ConstInts)(tiles + base + ii - nb * ntx);
+        tl.expert = t[0];
+        tl.row0 = t[1];
+        tl.rows = t[2];
+        tl.pad = 0;
     }
 };
 
