@@ -35,9 +35,9 @@ constexpr int kMaxTopK = 8;
 constexpr int kBlockTokensMin = 64;          // tokens per routing histogram block (at least)
 constexpr int kMaxBlocks = 64;               // histogram blocks per call (at most)
 constexpr int kHistCols = kMaxExperts + 1;   // experts + dropped slots
-constexpr int kMaxHidden = 4096;    // router stages x rows in LDS; GEMM scale blocks
+constexpr int kMaxHidden = 3072;    // router stages x rows in LDS; GEMM scale blocks
 constexpr int kTileRows = 32;       // rows per grouped-GEMM tile (2 x 16)
-constexpr int kBlockN = 128;        // weight rows per workgroup (4 waves x 32)
+constexpr int kBlockN = 256;        // weight rows per workgroup item (8 consumer waves x 32)
 constexpr int kChunkK = 256;        // k per LDS chunk of activations
 constexpr int kUnits = kChunkK / 8; // 16-byte units per LDS row
 
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void route_kernel(
         // ---- stage the x rows (rows past T repeat the last token); every
         // load is issued before the first store
         const int h8 = H / 8, n8 = TB * h8;
-        constexpr int NL = TB * (kMaxHidden / 8) / 256;
+        constexpr int NL = (TB * (kMaxHidden / 8) + 255) / 256;
         uint4 v[NL];
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
@@ -661,16 +661,16 @@ constexpr int kStageK = 256;     // k per stage (128 B of each weight row)
 constexpr int kAUnits = kTileRows * kUnits;  // 16-byte activation units per stage
 
 struct StageSlot {
-    uint8_t w[4][32 * 128];      // [consumer wave][32 rows x 128 B], swizzled
+    uint8_t w[8][32 * 128];      // [consumer wave][32 rows x 128 B], swizzled
     uint4 a[kAUnits];            // activations [row][unit ^ (row & 15)]
 };
 // e8m0 scales of one item: its 128 weight rows x K/32 bytes, copied whole
 // (contiguous in memory) by the consumers one item ahead; double-buffered.
 constexpr int kScaleBytes = kBlockN * (kMaxHidden / 32);
 
-// LDS row (0..31) of the wave's weight row wr (0..31): MLP1 puts gate rows
-// (even) in 0..15 and up rows (odd) in 16..31, so MFMA tile 0 / 1 lane n holds
-// gate / up of output column j = n; MLP2 keeps the order.
+// LDS row (0..31) of the consumer wave's weight row wr (0..31): MLP1 puts
+// gate rows (even) in 0..15 and up rows (odd) in 16..31, so MFMA column tile
+// 0 / 1 lane n holds gate / up of output column n; MLP2 keeps the order.
 template <bool kMlp1>
 __device__ __forceinline__ int lds_row_of(int wr) {
     return kMlp1 ? ((wr & 1) << 4) | (wr >> 1) : wr;
@@ -738,18 +738,18 @@ struct StepCursor {
     }
 };
 
-// Weight producer (waves 4, 5): rows 64 p .. 64 p + 63 of the block, 8 load
-// instructions of 8 rows x one full 128-byte row chunk per stage (lane l: row
-// 8 t + (l >> 3), chunk l & 7); kWDepth stages in flight (within the 63
-// outstanding loads a wave can track).  Invalid lanes write zeros.
+// Weight producer p (waves 8..11): rows 64 p .. 64 p + 63 of the block (the
+// rows of consumers 2 p, 2 p + 1), 8 load instructions of 8 rows x one full
+// 128-byte row chunk per stage (lane l: row 32 hh + 8 t + (l >> 3), chunk
+// l & 7); kWDepth stages in flight.  Invalid lanes write zeros.
 #ifndef GPTOSS_WDEPTH
-#define GPTOSS_WDEPTH 5
+#define GPTOSS_WDEPTH 3
 #endif
 constexpr int kWDepth = GPTOSS_WDEPTH;
 template <bool kMlp1>
 __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slots, int total,
                                                int total_p, const ItemMap &im, int NST) {
-    const int p = (threadIdx.x >> 6) - 4, lane = threadIdx.x & 63;
+    const int p = (threadIdx.x >> 6) - 8, lane = threadIdx.x & 63;  // 0..3
     const int rr = lane >> 3, ch = lane & 7;
     const int N = a.N, K = a.K;
     uint4 q[kWDepth][8];
@@ -767,15 +767,19 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
         const uint8_t *wq = a.Wq + (size_t)tl.expert * (seg_el / 2);
         const uint32_t k = (uint32_t)min(j * kStageK + 32 * ch, K - 32);
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {  // consumer region 2 p + hh
-            const int row0 = nb * kBlockN + (2 * p + hh) * 32;
+        for (int hh = 0; hh < 2; ++hh) {  // 32-row half hh of consumer region p
+            const int row0 = nb * kBlockN + 64 * p + 32 * hh;
             const bool wvalid = row0 < N;
             wval_of[r][hh] = wvalid;
             const uint32_t el0 = (uint32_t)(wvalid ? row0 + rr : 0) * (uint32_t)K + k;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint32_t el = el0 + t * 8u * (uint32_t)K;
+#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 1)
+                q[r][4 * hh + t] = make_uint4(el, el, 0, 0);  // timing diagnostic: no weight loads
+#else
                 q[r][4 * hh + t] = *reinterpret_cast<const uint4 *>(wq + el / 2);
+#endif
             }
         }
         stage_of[r] = j;
@@ -829,7 +833,7 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
     __syncthreads();  // iteration total_p: consumers finish the last step
 }
 
-// Activation loader (waves 6, 7): the stage's 32 x 256 activation chunk;
+// Activation loader (waves 12, 13): the stage's 32 x 256 activation chunk;
 // instruction i of loader p covers rows 4 i + 2 p + (0, 1) (two full 512-byte
 // row chunks; lane l: row + (l >> 5), 16-byte unit l & 31).  Loads are issued
 // kADepth stages ahead, as deep as the weights: the CU returns loads in
@@ -840,7 +844,7 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
 constexpr int kADepth = kWDepth;
 __device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots, int total,
                                              int total_p, const ItemMap &im, int NST) {
-    const int p = (threadIdx.x >> 6) - 6, lane = threadIdx.x & 63;
+    const int p = (threadIdx.x >> 6) - 12, lane = threadIdx.x & 63;
     const int c = lane & 31;
     const int K = a.K;
     u32x4 v[kADepth][8];
@@ -851,12 +855,18 @@ __device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots
         Tile tl;
         int nb, j;
         cursor.at(a, im, NST, st, tl, nb, j);
-        const int k = min(j * kStageK + 8 * c, K - 8);
-        const uint16_t *base = a.A + (size_t)tl.row0 * K + k;
+        // uniform base + 32-bit byte offsets (one VGPR per address)
+        const char *base = reinterpret_cast<const char *>(a.A + (size_t)tl.row0 * K);
+        const uint32_t kb = 2u * (uint32_t)min(j * kStageK + 8 * c, K - 8);
+        const int rmax = tl.rows - 1;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int row = min(4 * i + 2 * p + (lane >> 5), tl.rows - 1);
-            v[r][i] = *reinterpret_cast<const u32x4 *>(base + (uint32_t)row * (uint32_t)K);
+            const uint32_t off = (uint32_t)min(4 * i + 2 * p + (lane >> 5), rmax) * (2u * K) + kb;
+#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 2)
+            v[r][i] = u32x4{off, 0u, 0u, 0u};  // timing diagnostic: no activation loads
+#else
+            v[r][i] = *reinterpret_cast<const u32x4 *>(base + off);
+#endif
         }
     };
 #pragma unroll
@@ -898,23 +908,24 @@ __device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots
 // epilogue.  MT (row tiles of 16) is a template parameter so the
 // accumulators are plain registers with no guarded MFMAs (a guard around an
 // MFMA makes the compiler copy its accumulator in and out).
-// Item i's scale block: weight rows nb*128 .. +127 (those below N) of its
-// expert, K/32 bytes each, contiguous; 4 x 16 bytes per consumer lane.
+// Item i's scale block: weight rows nb*256 .. +255 (those below N) of its
+// expert, K/32 bytes each, contiguous; 3 x 16 bytes per consumer lane.
+constexpr int kScaleLoads = kScaleBytes / (512 * 16);
 __device__ __forceinline__ void scale_block_load(const GemmArgs &a, const Tile &tl, int nb,
-                                                 u32x4 (&v)[4]) {
+                                                 u32x4 (&v)[kScaleLoads]) {
     const int N = a.N, K = a.K;
     const int nrows = min(kBlockN, N - nb * kBlockN);
     const int len = nrows * (K / 32);  // multiple of 64 bytes
     const uint8_t *src = a.Ws + (size_t)tl.expert * ((size_t)N * K / 32) +
                          (size_t)nb * kBlockN * (K / 32);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-        v[u] = *reinterpret_cast<const u32x4 *>(src + min(16 * ((int)threadIdx.x + 256 * u), len - 16));
+    for (int u = 0; u < kScaleLoads; ++u)
+        v[u] = *reinterpret_cast<const u32x4 *>(src + min(16 * ((int)threadIdx.x + 512 * u), len - 16));
 }
-__device__ __forceinline__ void scale_block_store(uint8_t *dst, const u32x4 (&v)[4]) {
+__device__ __forceinline__ void scale_block_store(uint8_t *dst, const u32x4 (&v)[kScaleLoads]) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-        *reinterpret_cast<u32x4 *>(dst + 16 * ((int)threadIdx.x + 256 * u)) = v[u];
+    for (int u = 0; u < kScaleLoads; ++u)
+        *reinterpret_cast<u32x4 *>(dst + 16 * ((int)threadIdx.x + 512 * u)) = v[u];
 }
 
 template <int MT, bool kMlp1>
@@ -926,7 +937,7 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
     const int n_l = lane & 15, g = lane >> 4;
     const int N = a.N;
     const int KS = a.K / 32;
-    u32x4 nsv[4];
+    u32x4 nsv[kScaleLoads];
     if (has_next) scale_block_load(a, ntl, nnb, nsv);
     f32x4 acc[MT][2];
 #pragma unroll
@@ -935,14 +946,6 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
         TR_T0
         const StageSlot &sl = slots[s & 1];
         const uint8_t *wb = sl.w[wave];
-#if defined(GPTOSS_DIAG) && GPTOSS_DIAG == 2
-        {
-            const uint4 v = sl.a[lane * 16];
-            const uint4 w = *reinterpret_cast<const uint4 *>(wb + 16 * lane);
-            acc[0][0][0] += __uint_as_float((v.x ^ w.y ^ sb[lane]) & 0x3fffffffu);
-        }
-        if (0)
-#endif
 
         {
 #pragma unroll
@@ -981,8 +984,9 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     const bf16x8 af = __builtin_bit_cast(bf16x8, av[m][qd]);
-                    acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[0], acc[m][0], 0, 0, 0);
-                    acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[1], acc[m][1], 0, 0, 0);
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt)
+                        acc[m][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[tt], acc[m][tt], 0, 0, 0);
                 }
             }
         }
@@ -994,24 +998,27 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
             if (wcol0 < N) {
                 if (kMlp1) {
                     const int D = N / 2;
-                    const int jc = wcol0 / 2 + n_l;
-                    const float bg = bf2f(a.bias[(size_t)e * N + 2 * jc]);
-                    const float bu = bf2f(a.bias[(size_t)e * N + 2 * jc + 1]);
 #pragma unroll
-                    for (int m = 0; m < MT; ++m)
+                    for (int t2 = 0; t2 < 1; ++t2) {  // gate tile 0, up tile 1
+                        const int jc = wcol0 / 2 + n_l;
+                        const float bg = bf2f(a.bias[(size_t)e * N + 2 * jc]);
+                        const float bu = bf2f(a.bias[(size_t)e * N + 2 * jc + 1]);
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const int r = m * 16 + 4 * g + v;
-                            if (r < tl.rows) {
-                                float gt = bf16_round(acc[m][0][v] + bg);
-                                float up = bf16_round(acc[m][1][v] + bu);
-                                gt = fminf(fmaxf(gt, -a.limit), a.limit);
-                                up = fminf(fmaxf(up, -a.limit), a.limit);
-                                const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
-                                gt = gt * sig;
-                                a.out_act[(size_t)(tl.row0 + r) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                        for (int m = 0; m < MT; ++m)
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) {
+                                const int r = m * 16 + 4 * g + v;
+                                if (r < tl.rows) {
+                                    float gt = bf16_round(acc[m][t2][v] + bg);
+                                    float up = bf16_round(acc[m][t2 + 1][v] + bu);
+                                    gt = fminf(fmaxf(gt, -a.limit), a.limit);
+                                    up = fminf(fmaxf(up, -a.limit), a.limit);
+                                    const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
+                                    gt = gt * sig;
+                                    a.out_act[(size_t)(tl.row0 + r) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                                }
                             }
-                        }
+                    }
                 } else {
                     const int H = N;
                     int slot[MT][4];  // token-order slot of each of this lane's rows
@@ -1029,8 +1036,8 @@ __device__ __forceinline__ void consume_item(const GemmArgs &a, const StageSlot 
                         for (int v = 0; v < 4; ++v) {
                             if (m * 16 + 4 * g + v < tl.rows) {
                                 uint16_t *dst = a.out_slots + (size_t)slot[m][v] * H + wcol0 + n_l;
-                                dst[0] = f2bf(acc[m][0][v] + bb[0]);
-                                dst[16] = f2bf(acc[m][1][v] + bb[1]);
+#pragma unroll
+                                for (int t = 0; t < 2; ++t) dst[16 * t] = f2bf(acc[m][t][v] + bb[t]);
                             }
                         }
                 }
@@ -1054,7 +1061,7 @@ __device__ __forceinline__ void gemm_consumer(const GemmArgs &a, StageSlot *slot
     int nb, nnb;
     im.at(a.tiles, 0, tl, nb);
     {
-        u32x4 v[4];
+        u32x4 v[kScaleLoads];
         scale_block_load(a, tl, nb, v);
         scale_block_store(sscale[0], v);
     }
@@ -1075,8 +1082,9 @@ __device__ __forceinline__ void gemm_consumer(const GemmArgs &a, StageSlot *slot
     for (; s < total_p; ++s) __syncthreads();  // producers' padding steps
 }
 
+constexpr int kSmallWaves = 14;  // 8 consumers, 4 weight producers, 2 activation loaders
 template <bool kMlp1>
-__global__ __launch_bounds__(512) void grouped_gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kSmallWaves * 64) void grouped_gemm_kernel(GemmArgs a) {
     __shared__ StageSlot slots[2];
     __shared__ __attribute__((aligned(16))) uint8_t sscale[2][kScaleBytes];
     ItemMap im;
@@ -1087,12 +1095,328 @@ __global__ __launch_bounds__(512) void grouped_gemm_kernel(GemmArgs a) {
     const int total = n_items * NST;
     const int total_p = (total + kWDepth - 1) / kWDepth * kWDepth;
     const int wave = threadIdx.x >> 6;
-    if (wave < 4)
+#ifdef GPTOSS_TRACE
+    const unsigned long long c0 = __builtin_readcyclecounter(), r0 = __builtin_amdgcn_s_memrealtime();
+#endif
+    if (wave < 8)
         gemm_consumer<kMlp1>(a, slots, sscale, n_items, total_p, im, NST);
-    else if (wave < 6)
+    else if (wave < 12)
         gemm_wproducer<kMlp1>(a, slots, total, total_p, im, NST);
     else
         gemm_aloader(a, slots, total, total_p, im, NST);
+#ifdef GPTOSS_TRACE
+    if (threadIdx.x == 0) {  // shader clock vs 100 MHz real-time clock over the workgroup
+        unsigned long long *t = reinterpret_cast<unsigned long long *>(const_cast<int32_t *>(a.hdr) + 128);
+        atomicAdd(t + (kMlp1 ? 60 : 62), __builtin_readcyclecounter() - c0);
+        atomicAdd(t + (kMlp1 ? 61 : 63), __builtin_amdgcn_s_memrealtime() - r0);
+    }
+#endif
+}
+
+// ------------------------------------------------ large-M grouped GEMM --
+//
+// For experts with many rows (prefill).  An item is (tile of up to 128 rows of
+// one expert, block of 256 weight rows); one 8-wave workgroup per CU walks its
+// items' K stages (128 k each) without draining.  All 512 threads load: the
+// stage's 128 x 128 activation chunk (bf16), the block's 256 x 128 weight
+// chunk (MXFP4 nibbles, 64 B per row) with its e8m0 scales, and the block's
+// bias and the tile's token slots, through a kLRing-deep register ring into
+// double-buffered LDS.  Wave (wm, wn) = (w & 1, w >> 1) computes tile rows
+// 64 wm .. +63 x weight rows 64 wn .. +63 with v_mfma_f32_32x32x16_bf16 (2 x 2
+// fragments) and dequantises its own weight fragments from the LDS nibbles
+// (each weight is dequantised by the 2 waves that share its rows).
+//
+// MFMA 32x32x16: lane l = (n = l & 31, g = l >> 5) supplies A[row n][8 g + e]
+// and B[8 g + e][column n]; in k step s of stage j, slot (g, e) stands for
+// k = 128 j + 64 g + 8 s + e (a permutation of k shared by both operands).
+// Output: lane holds C[8 (v >> 2) + 4 g + (v & 3)][n], v = 0..15.
+// MLP1: the block's gate rows (even) sit in LDS rows 0..127 and its up rows
+// (odd) in 128..255, so column fragment 0 / 1 of wave wn holds gate / up of
+// output column nb * 128 + 32 wn + n in the same lane.
+constexpr int kLBM = 128, kLBN = 256, kLBK = 128;
+constexpr int kLRing = 3;
+constexpr int kLWaves = 8;
+constexpr int kLMaxTiles = 512;  // tiles per XCD
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+struct LStage {
+    uint4 a[kLBM * (kLBK / 8)];   // tile row r, 16-byte unit u at r * 16 + (u ^ (r & 15))
+    uint4 b[kLBN * (kLBK / 32)];  // LDS row R, unit u at R * 4 + (u ^ ((R >> 2) & 3))
+    uint32_t s[kLBN];             // e8m0 of LDS row R, k groups 4 j .. 4 j + 3 (byte q)
+    uint16_t bias[kLBN];          // bias of LDS row R
+    int32_t slot[kLBM];           // MLP2: token-order slot of tile row r
+};
+struct LTile {
+    int expert, row0, rows, pad;
+};
+
+template <bool kMlp1>
+__device__ __forceinline__ int lrow_of(int r) {  // weight row (in block) -> LDS row
+    return kMlp1 ? ((r & 1) << 7) | (r >> 1) : r;
+}
+
+template <bool kMlp1>
+__global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
+                                                                   const int32_t *__restrict__ counts,
+                                                                   const int32_t *__restrict__ offsets,
+                                                                   int E) {
+    __shared__ LStage buf[2];
+    __shared__ LTile tiles[kLMaxTiles];
+    __shared__ int s_ntiles;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int N = a.N, K = a.K, KS = K / 32;
+    const int nblk = (N + kLBN - 1) / kLBN;
+    const int NST = (K + kLBK - 1) / kLBK;
+    const int xcd = (int)blockIdx.x & 7, wg = (int)blockIdx.x >> 3, Gx = (int)gridDim.x >> 3;
+
+    // ---- this XCD's tiles: experts e = xcd, xcd + 8, ...; 128 rows + remainder
+    if (wave == 0) {
+        int n = 0;
+        for (int e0 = xcd; e0 < E; e0 += 8 * 64) {
+            const int e = e0 + 8 * lane;
+            const int c = e < E ? counts[e] : 0;
+            const int o = e < E ? offsets[e] : 0;
+            const int nt = (c + kLBM - 1) / kLBM;
+            const int inc = wave_scan(nt, lane);
+            const int base = n + inc - nt;
+            for (int m = 0; m < nt; ++m)
+                if (base + m < kLMaxTiles)
+                    tiles[base + m] = LTile{e, o + m * kLBM, min(kLBM, c - m * kLBM), 0};
+            n += __shfl(inc, 63, 64);
+        }
+        if (lane == 0) s_ntiles = min(n, kLMaxTiles);
+    }
+    __syncthreads();
+    const int ntx = s_ntiles;
+    const int items_x = ntx * nblk;
+    const int n_items = items_x > wg ? (items_x - wg + Gx - 1) / Gx : 0;
+    if (n_items == 0) return;
+    const int total = n_items * NST;
+    const int total_p = (total + kLRing - 1) / kLRing * kLRing;
+
+    auto stage_at = [&](int st, LTile &tl, int &nb, int &j) {
+        const int i = st / NST;
+        j = st - i * NST;
+        const int ii = wg + i * Gx;
+        const int ti = ii / nblk;
+        nb = ii - ti * nblk;
+        tl = tiles[ti];
+    };
+
+    // ---- loads: per thread 4 activation units, 2 weight units, 2 halfwords
+    u32x4 ra[kLRing][4];
+    u32x4 rb[kLRing][2];
+    uint32_t rx[kLRing][2];
+    auto issue = [&](int st, int r) {
+        st = min(st, total - 1);
+        LTile tl;
+        int nb, j;
+        stage_at(st, tl, nb, j);
+        const char *abase = reinterpret_cast<const char *>(a.A + (size_t)tl.row0 * K);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 512 * i, row = q >> 4, u = q & 15;
+            const uint32_t off = (uint32_t)min(row, tl.rows - 1) * (2u * K) +
+                                 2u * (uint32_t)min(j * kLBK + 8 * u, K - 8);
+#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 2)
+            ra[r][i] = u32x4{off, 0u, 0u, 0u};  // timing diagnostic: no activation loads
+#else
+            ra[r][i] = *reinterpret_cast<const u32x4 *>(abase + off);
+#endif
+        }
+        const uint8_t *wq = a.Wq + (size_t)tl.expert * ((size_t)N * K / 2);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
+            const uint32_t row = (uint32_t)min(nb * kLBN + r0, N - 1);
+            const uint32_t kb = (uint32_t)min(j * (kLBK / 2) + 16 * u, K / 2 - 16);
+#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 1)
+            rb[r][i] = u32x4{row, kb, 0u, 0u};  // timing diagnostic: no weight loads
+#else
+            rb[r][i] = *reinterpret_cast<const u32x4 *>(wq + row * (uint32_t)(K / 2) + kb);
+#endif
+        }
+        // waves 0..3: scales of block row tid; 4, 5: bias pair; 6, 7: token slot
+        const uint16_t *p16;
+        if (wave < 4) {
+            const uint32_t row = (uint32_t)min(nb * kLBN + tid, N - 1);
+            p16 = reinterpret_cast<const uint16_t *>(a.Ws + (size_t)tl.expert * ((size_t)N * KS) +
+                                                     row * (uint32_t)KS + min(4 * j, KS - 4));
+        } else if (wave < 6) {
+            const int r0 = 2 * (tid - 256);
+            p16 = a.bias + (size_t)tl.expert * N + min(nb * kLBN + r0, N - 2);
+        } else {
+            const int r0 = tid - 384;
+            p16 = kMlp1 ? a.bias : reinterpret_cast<const uint16_t *>(a.row_slot + tl.row0 + min(r0, tl.rows - 1));
+        }
+        rx[r][0] = p16[0];
+        rx[r][1] = p16[1];
+    };
+    auto write = [&](int st, int r, LStage &sb) {
+        st = min(st, total - 1);
+        LTile tl;
+        int nb, j;
+        stage_at(st, tl, nb, j);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 512 * i, row = q >> 4, u = q & 15;
+            sb.a[row * 16 + (u ^ (row & 15))] = __builtin_bit_cast(uint4, ra[r][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
+            const int R = lrow_of<kMlp1>(r0);
+            const uint32_t km = -(uint32_t)(nb * kLBN + r0 < N && j * kLBK + 32 * u < K);
+            const u32x4 v = rb[r][i];
+            sb.b[R * 4 + (u ^ ((R >> 2) & 3))] = make_uint4(v.x & km, v.y & km, v.z & km, v.w & km);
+        }
+        if (wave < 4) {
+            // groups past K/32 (last stage) read as scale 0: weights there are zero
+            uint32_t sv = rx[r][0] | (rx[r][1] << 16);
+            const int ng = KS - 4 * j;  // valid groups of this stage (>= 2, K a multiple of 64)
+            if (ng < 4) sv = (sv >> (8 * (4 - ng))) & (ng >= 2 ? 0xffffu : 0u);
+            sb.s[lrow_of<kMlp1>(tid)] = sv;
+        } else if (wave < 6) {
+            const int r0 = 2 * (tid - 256);
+            sb.bias[lrow_of<kMlp1>(r0)] = (uint16_t)rx[r][0];
+            sb.bias[lrow_of<kMlp1>(r0 + 1)] = (uint16_t)rx[r][1];
+        } else if (!kMlp1) {
+            sb.slot[tid - 384] = (int32_t)(rx[r][0] | (rx[r][1] << 16));
+        }
+    };
+
+    // ---- compute state
+    const int wm = wave & 1, wn = wave >> 1;
+    const int n_l = lane & 31, g = lane >> 5;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[f][c][v] = 0.f;
+
+    auto compute = [&](int st, const LStage &sb) {
+        LTile tl;
+        int nb, j;
+        stage_at(st, tl, nb, j);
+        const int nf = min(2, max(0, (tl.rows - 64 * wm + 31) / 32));
+        uint4 bw[2][2];
+        uint32_t se[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int R = kMlp1 ? c * 128 + 32 * wn + n_l : 64 * wn + 32 * c + n_l;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) bw[c][h] = sb.b[R * 4 + ((2 * g + h) ^ ((R >> 2) & 3))];
+            se[c] = sb.s[R] >> (16 * g);  // groups 2 g, 2 g + 1
+        }
+        if (nf > 0) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                bf16x8 bq[2];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const uint32_t e = (se[c] >> (8 * (s >> 2))) & 0xffu;
+                    const uint32_t zm = e == 0 ? 0x88888888u : 0xffffffffu;
+                    const uint4 v = bw[c][s >> 2];
+                    const uint32_t dw = (s & 3) == 0 ? v.x : (s & 3) == 1 ? v.y : (s & 3) == 2 ? v.z : v.w;
+#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 4)
+                    bq[c] = __builtin_bit_cast(bf16x8, u32x4{dw, dw ^ zm, e, dw ^ 3u});  // timing diagnostic
+#else
+                    bq[c] = dequant8(dw & zm, e8m0_to_f32(e));
+#endif
+                }
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    if (f < nf) {
+                        const int row = 64 * wm + 32 * f + n_l;
+                        const bf16x8 av = __builtin_bit_cast(bf16x8, sb.a[row * 16 + ((8 * g + s) ^ (row & 15))]);
+#pragma unroll
+                        for (int c = 0; c < 2; ++c) {
+#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 8)
+                            const u32x4 x0 = __builtin_bit_cast(u32x4, av), y0 = __builtin_bit_cast(u32x4, bq[c]);
+                            acc[f][c][0] += __uint_as_float((x0.x ^ y0.y ^ x0.z ^ y0.w) & 0x3fffffffu);  // timing diagnostic
+#else
+                            acc[f][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bq[c], acc[f][c], 0, 0, 0);
+#endif
+                        }
+                    }
+                }
+            }
+        }
+        if (j == NST - 1) {
+            // ---- epilogue of the item
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                if (f < nf) {
+                    if (kMlp1) {
+                        const int D = N / 2;
+                        const int jc = nb * (kLBN / 2) + 32 * wn + n_l;
+                        const float bg = bf2f(sb.bias[32 * wn + n_l]);
+                        const float bu = bf2f(sb.bias[128 + 32 * wn + n_l]);
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int row = 64 * wm + 32 * f + 8 * (v >> 2) + 4 * g + (v & 3);
+                            if (row < tl.rows && jc < D) {
+                                float gt = bf16_round(acc[f][0][v] + bg);
+                                float up = bf16_round(acc[f][1][v] + bu);
+                                gt = fminf(fmaxf(gt, -a.limit), a.limit);
+                                up = fminf(fmaxf(up, -a.limit), a.limit);
+                                const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
+                                gt = gt * sig;
+                                a.out_act[(size_t)(tl.row0 + row) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 2; ++c) {
+                            const int R = 64 * wn + 32 * c + n_l;
+                            const int h = nb * kLBN + R;
+                            const float bb = bf2f(sb.bias[R]);
+#pragma unroll
+                            for (int v = 0; v < 16; ++v) {
+                                const int row = 64 * wm + 32 * f + 8 * (v >> 2) + 4 * g + (v & 3);
+                                if (row < tl.rows && h < N)
+                                    a.out_slots[(size_t)sb.slot[row] * N + h] = f2bf(acc[f][c][v] + bb);
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[f][c][v] = 0.f;
+        }
+    };
+
+    // ---- pipeline: stage s computed from buf s & 1 while stage s + 1 is
+    // written into the other buffer; loads run kLRing stages ahead
+#pragma unroll
+    for (int r = 0; r < kLRing; ++r) {
+        issue(r, r);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    write(0, 0, buf[0]);
+    issue(kLRing, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    for (int s0 = 0; s0 < total_p; s0 += kLRing) {
+#pragma unroll
+        for (int r = 0; r < kLRing; ++r) {
+            const int s = s0 + r;
+            __builtin_amdgcn_sched_barrier(0);
+            if (s < total) compute(s, buf[s & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            const int rn = (r + 1) % kLRing;  // constant once unrolled
+            write(s + 1, rn, buf[(s + 1) & 1]);
+            issue(s + 1 + kLRing, rn);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        }
+    }
 }
 
 // Weighted top-k reduction (reduce_tokenwise_expert_outputs_bf16_bf16wts,
@@ -1235,6 +1559,9 @@ bool shape_ok(const gptoss_moe_shape *s) {
     return true;
 }
 
+constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SMALL_M_GEMM |
+                               GPTOSS_MOE_FLAG_LARGE_M_GEMM;
+
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 struct Ptrs {
@@ -1349,6 +1676,18 @@ int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const u
     return hip_status(hipGetLastError());
 }
 
+// Large-M GEMM when experts average >= 96 rows (or when forced), and the shape
+// fits its staging: K >= 256 (whole 4-byte scale reads), and at most
+// kLMaxTiles 128-row tiles per XCD whatever the routing.
+bool use_large_m(const gptoss_moe_shape *s, int T, unsigned flags) {
+    const long P = (long)T * s->top_k;
+    const bool fits = s->hidden >= 256 && s->intermediate >= 256 &&
+                      P / kLBM + s->n_experts / 8 + 1 <= kLMaxTiles;
+    if (!fits || (flags & GPTOSS_MOE_FLAG_SMALL_M_GEMM)) return false;
+    if (flags & GPTOSS_MOE_FLAG_LARGE_M_GEMM) return true;
+    return P >= 96L * s->n_experts;
+}
+
 int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                    uint16_t *out, int T, unsigned flags, const WsLayout &L, const Ptrs &p,
                    hipStream_t st, Marks *mk = nullptr) {
@@ -1370,9 +1709,12 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a1.K = H;
     a1.limit = s->swiglu_limit;
     a1.alpha = s->swiglu_alpha;
-    const int max_tiles = (int)((size_t)T * s->top_k / 16 + s->n_experts + 1);
-    const int items1 = max_tiles * ((2 * D + kBlockN - 1) / kBlockN);
-    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(512), 0, st, a1);
+    const bool large = use_large_m(s, T, flags);
+    if (large)
+        hipLaunchKernelGGL(large_m_gemm_kernel<true>, dim3(cap), dim3(kLWaves * 64), 0, st, a1,
+                           p.counts, p.offsets, s->n_experts);
+    else
+        hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a1);
     if (mk) mk->mark(st);
 
     GemmArgs a2 = a1;
@@ -1384,8 +1726,11 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a2.out_slots = p.slots;
     a2.N = H;
     a2.K = D;
-    const int items2 = max_tiles * ((H + kBlockN - 1) / kBlockN);
-    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(512), 0, st, a2);
+    if (large)
+        hipLaunchKernelGGL(large_m_gemm_kernel<false>, dim3(cap), dim3(kLWaves * 64), 0, st, a2,
+                           p.counts, p.offsets, s->n_experts);
+    else
+        hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a2);
     if (mk) mk->mark(st);
 
     const size_t n8 = (size_t)T * H / 8;
@@ -1457,7 +1802,7 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     int rc = check_common(shape, w, n_tokens, forced_topk_i, forced_topk_w, workspace, ws_bytes,
                           max_tokens);
     if (rc) return rc;
-    if (flags & ~(unsigned)GPTOSS_MOE_FLAG_RESIDUAL_ADD) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
     if (!w->w1 || !w->w1_scales || !w->b1 || !w->w2 || !w->w2_scales || !w->b2)
         return GPTOSS_MOE_ERR_INVALID_ARG;
     if (!aligned16(w->w1) || !aligned16(w->w2)) return GPTOSS_MOE_ERR_INVALID_ARG;
@@ -1479,7 +1824,7 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
                           max_tokens);
     if (rc) return rc;
     if (!kernel_ms || n_tokens == 0 || !x_norm || !out) return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (flags & ~(unsigned)GPTOSS_MOE_FLAG_RESIDUAL_ADD) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
     Marks mk;
     mk.on = true;
     for (int i = 0; i < 6; ++i)

@@ -26,6 +26,9 @@ ERR_WORKSPACE = -2
 ERR_HIP = -3
 ERR_UNSUPPORTED = -4
 FLAG_RESIDUAL_ADD = 1
+FLAG_SMALL_M_GEMM = 2
+FLAG_LARGE_M_GEMM = 4
+_PATH_FLAGS = {"auto": 0, "small": FLAG_SMALL_M_GEMM, "large": FLAG_LARGE_M_GEMM}
 
 _ERRNAMES = {ERR_INVALID_ARG: "invalid argument", ERR_WORKSPACE: "workspace too small",
              ERR_HIP: "HIP error", ERR_UNSUPPORTED: "unsupported shape"}
@@ -167,27 +170,30 @@ class MoeLayer:
 
     # -- entry points ---------------------------------------------------
     def forward(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,
-                stream=None):
-        """e_agg (or out + e_agg with residual=True) for bf16 rows x_norm [T][H]."""
+                stream=None, path="auto"):
+        """e_agg (or out + e_agg with residual=True) for bf16 rows x_norm [T][H].
+        path: "auto", or "small" / "large" to force the grouped-GEMM path."""
         import torch
         T = x_norm.shape[0]
         if out is None:
             out = torch.empty_like(x_norm)
         rc = self.lib.gptoss_moe_forward(
             ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(x_norm), _ptr(out), T,
-            _ptr(forced_i), _ptr(forced_w), FLAG_RESIDUAL_ADD if residual else 0,
+            _ptr(forced_i), _ptr(forced_w),
+            (FLAG_RESIDUAL_ADD if residual else 0) | _PATH_FLAGS[path],
             self.ws.data_ptr(), self.ws_bytes, self.max_tokens, _stream(stream))
         _check("gptoss_moe_forward", rc)
         return out
 
     KERNELS = ("route", "index", "mlp1", "mlp2", "finalize")
 
-    def forward_profiled(self, x_norm, out, forced_i=None, forced_w=None, stream=None) -> dict:
+    def forward_profiled(self, x_norm, out, forced_i=None, forced_w=None, stream=None,
+                         path="auto") -> dict:
         """forward() with per-kernel HIP-event durations (ms); synchronises."""
         ms = (ctypes.c_float * 5)()
         rc = self.lib.gptoss_moe_forward_profiled(
             ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(x_norm), _ptr(out),
-            x_norm.shape[0], _ptr(forced_i), _ptr(forced_w), 0, self.ws.data_ptr(),
+            x_norm.shape[0], _ptr(forced_i), _ptr(forced_w), _PATH_FLAGS[path], self.ws.data_ptr(),
             self.ws_bytes, self.max_tokens, _stream(stream), ms)
         _check("gptoss_moe_forward_profiled", rc)
         return dict(zip(self.KERNELS, list(ms)))

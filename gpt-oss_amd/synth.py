@@ -46,6 +46,8 @@ CONFIGS = {
     "c2_20b_zipf": MoeConfig("c2_20b_zipf", 2880, 2880, 32, 4, 512, "zipf", 0x6F550002),
     "c3a_120b_decode": MoeConfig("c3a_120b_decode", 2880, 2880, 128, 4, 1024, "uniform", 0x6F550003),
     "c3b_120b_prefill": MoeConfig("c3b_120b_prefill", 2880, 2880, 128, 4, 4096, "router", 0x6F550004),
+    # test-only: many rows per expert at a small shape (large-M GEMM path, ragged tiles)
+    "t_large_m": MoeConfig("t_large_m", 384, 320, 6, 2, 700, "router", 0x6F550010),
 }
 
 

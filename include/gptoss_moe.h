@@ -40,11 +40,18 @@ extern "C" {
 /* out[t][h] = bf16(out[t][h] + e_agg[t][h]) instead of out = e_agg
  * (the residual update of other_kernels.hpp:17-35). */
 #define GPTOSS_MOE_FLAG_RESIDUAL_ADD 1u
+/* GEMM path selection (no counterpart in the reference, which picks its tile
+ * shape from the largest expert count, getp_run.cpp:2666).  By default the
+ * large-M path (128-row tiles) runs when experts average >= 96 rows; these
+ * force either path.  The large-M path needs hidden, intermediate >= 256 and
+ * falls back to the small-M path otherwise. */
+#define GPTOSS_MOE_FLAG_SMALL_M_GEMM 2u
+#define GPTOSS_MOE_FLAG_LARGE_M_GEMM 4u
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {
-    int hidden;        /* H = Config.hidden_dim; multiple of 64 */
-    int intermediate;  /* D = Config.intermediate_dim; multiple of 64 */
+    int hidden;        /* H = Config.hidden_dim; multiple of 64, at most 3072 */
+    int intermediate;  /* D = Config.intermediate_dim; multiple of 64, at most 3072 */
     int n_experts;     /* E = Config.n_experts; 1..256 */
     int top_k;         /* k = Config.experts_per_token; 1..8, <= E */
     float swiglu_limit; /* Config.swiglu_limit (7.0 for gpt-oss) */

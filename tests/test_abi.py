@@ -80,9 +80,9 @@ def test_argument_errors_without_gpu():
     # unknown flag bits
     need = gm.workspace_size(s, 8)
     assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
-                                  2, fake, need, 8, None) == gm.ERR_INVALID_ARG
-    # hidden beyond the router's register budget
-    big = gm.make_shape(4096 + 64, 128, 4, 2)
+                                  8, fake, need, 8, None) == gm.ERR_INVALID_ARG
+    # hidden beyond the supported envelope (LDS staging of router rows and scale blocks)
+    big = gm.make_shape(3072 + 64, 128, 4, 2)
     assert lib.gptoss_moe_route(ctypes.byref(big), ctypes.byref(w), None, 4, None, None, fake,
                                 1 << 40, 8, None) == gm.ERR_UNSUPPORTED
     assert lib.gptoss_moe_rmsnorm(None, None, None, 1, 8, None) == gm.ERR_INVALID_ARG

@@ -6,25 +6,25 @@ gemm_aloader and scale_block_load), vectorised over lanes, stages and rows."""
 import numpy as np
 import pytest
 
-BLOCK_N = 128
+BLOCK_N = 256
 STAGE_K = 256
 
 
 def wproducer_loads(N, K):
     """Byte offsets of the weight producer's 16-byte nibble loads into one
-    expert's N*K/2 bytes (gemm_wproducer: lane l loads row 8 t + (l >> 3),
-    chunk l & 7; invalid row blocks read row 0)."""
+    expert's N*K/2 bytes (gemm_wproducer, 4 producers of 64 rows: lane l loads
+    row 64 p + 32 hh + 8 t + (l >> 3), chunk l & 7; invalid halves read row 0)."""
     nst = (K + STAGE_K - 1) // STAGE_K
     nblk = (N + BLOCK_N - 1) // BLOCK_N
     q = []
     lane = np.arange(64)
     rr, ch = lane >> 3, lane & 7
     for nb in range(nblk):
-        for p in range(2):
+        for p in range(4):
             for j in range(nst):
                 k = np.minimum(j * STAGE_K + 32 * ch, K - 32)
                 for hh in range(2):
-                    row0 = nb * BLOCK_N + (2 * p + hh) * 32
+                    row0 = nb * BLOCK_N + 64 * p + 32 * hh
                     wvalid = row0 < N
                     el0 = np.where(wvalid, row0 + rr, 0) * K + k
                     for t in range(4):
@@ -34,16 +34,16 @@ def wproducer_loads(N, K):
 
 def scale_block_loads(N, K):
     """Byte offsets of the consumers' 16-byte loads of one item's scale block
-    (scale_block_load: 256 consumer threads x 4 loads, clamped to the block)."""
+    (scale_block_load: 512 consumer threads x 3 loads, clamped to the block)."""
     out = []
-    tid = np.arange(256)
+    tid = np.arange(512)
     for nb in range((N + BLOCK_N - 1) // BLOCK_N):
         nrows = min(BLOCK_N, N - nb * BLOCK_N)
         length = nrows * (K // 32)
         # the block must fit the LDS copy the consumers read from
-        assert length <= 4 * 256 * 16
-        for u in range(4):
-            out.append(nb * BLOCK_N * (K // 32) + np.minimum(16 * (tid + 256 * u), length - 16))
+        assert length <= 3 * 512 * 16
+        for u in range(3):
+            out.append(nb * BLOCK_N * (K // 32) + np.minimum(16 * (tid + 512 * u), length - 16))
     return np.concatenate(out)
 
 
@@ -64,7 +64,7 @@ def aloader_loads(K, row0, rows):
 
 
 @pytest.mark.parametrize("N,K", [(256, 128), (128, 128), (64, 64), (5760, 2880), (2880, 2880),
-                                 (128, 64), (192, 320), (320, 192), (8192, 4096), (4096, 4096)])
+                                 (128, 64), (192, 320), (320, 192), (6144, 3072), (3072, 3072)])
 def test_weight_and_scale_loads_in_bounds(N, K):
     q = wproducer_loads(N, K)
     s = scale_block_loads(N, K)
@@ -130,3 +130,36 @@ def test_tile_placement_is_a_balanced_bijection(seed):
     assert sorted(placed) == list(range(total))
     assert max(xcount) - min(xcount) <= 2
     assert all(len(v) == 1 for v in unit_xcd.values())  # a unit's tiles share an XCD
+
+
+# ------------------------------------------------------------ large-M GEMM --
+LBN, LBK = 256, 128
+
+
+def large_m_weight_loads(N, K):
+    """large_m_gemm_kernel issue(): per thread 2 x 16-byte nibble loads (block
+    row q >> 2, unit q & 3 of the stage's 64-byte row chunk) and one 4-byte scale
+    read as two halfwords (waves 0..3: block row tid, groups 4 j .. 4 j + 3)."""
+    nst = (K + LBK - 1) // LBK
+    KS = K // 32
+    q, s = [], []
+    tid = np.arange(512)
+    for nb in range((N + LBN - 1) // LBN):
+        for j in range(nst):
+            for i in range(2):
+                qq = tid + 512 * i
+                row = np.minimum(nb * LBN + (qq >> 2), N - 1)
+                kb = np.minimum(j * (LBK // 2) + 16 * (qq & 3), K // 2 - 16)
+                q.append(row * (K // 2) + kb)
+            row = np.minimum(nb * LBN + tid[:256], N - 1)
+            s.append(row * KS + min(4 * j, KS - 4))
+    return np.concatenate(q), np.concatenate(s)
+
+
+@pytest.mark.parametrize("N,K", [(5760, 2880), (2880, 2880), (640, 384), (384, 320), (512, 256),
+                                 (6144, 3072)])
+def test_large_m_loads_in_bounds(N, K):
+    q, s = large_m_weight_loads(N, K)
+    assert q.min() >= 0 and (q + 16).max() <= N * K // 2 and (q % 16 == 0).all()
+    # 4 scale bytes inside the expert's N*K/32, 2-byte aligned (two halfword loads)
+    assert s.min() >= 0 and (s + 4).max() <= N * K // 32 and (s % 2 == 0).all()

@@ -127,14 +127,14 @@ def test_routing_invalid_and_duplicate_slots(gpu):
 
 
 # ---------------------------------------------------------------- forward --
-def _forward(d, gpu, rows_check=None, residual=False):
+def _forward(d, gpu, rows_check=None, residual=False, path="auto"):
     import gptoss_moe
     c = d.cfg
     layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
     x = _dev(d.x, gpu)
     fi = None if d.forced_i is None else _dev(d.forced_i, gpu)
     fw = None if d.forced_w is None else _dev(d.forced_w, gpu)
-    out = layer.forward(x, forced_i=fi, forced_w=fw)
+    out = layer.forward(x, forced_i=fi, forced_w=fw, path=path)
     got = _host16(out)
     ref = oracle.moe_forward(d, forced=d.forced_i is not None, rows=rows_check)
     sel = slice(None) if rows_check is None else rows_check
@@ -153,6 +153,17 @@ def test_forward_120b_decode(gpu):
     d = _data("c3a_120b_decode")
     _, _, _, m = _forward(d, gpu)
     print(m)
+
+
+@pytest.mark.parametrize("name,path", [("t_large_m", "auto"), ("t_large_m", "small"),
+                                       ("c1_20b_decode", "large"), ("c2_20b_zipf", "large")])
+def test_forward_gemm_paths(gpu, name, path):
+    """Both grouped-GEMM paths against the oracle: the large-M path on ragged
+    128-row tiles (t_large_m), on small experts (c1) and on skewed routing with
+    multi-tile experts (c2); the small-M path where large-M would run."""
+    d = _data(name)
+    _, _, _, m = _forward(d, gpu, path=path)
+    print(name, path, m)
 
 
 def test_forward_120b_prefill_sampled(gpu):
