@@ -181,7 +181,7 @@ def main():
         "config": {"workload": c.name, "hidden": H, "intermediate": D, "n_experts": c.n_experts,
                    "top_k": c.top_k, "tokens": c.tokens, "routing": c.routing,
                    "weight_copies_rotated": copies},
-        "roofline": {"bound": "hbm", "kernel": "grouped_gemm_kernel<mlp1>",
+        "roofline": {"bound": "hbm", "kernel": "direct_gemm_kernel<true> (MLP1)",
                      "achieved": round(mlp1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": mlp1_bytes,

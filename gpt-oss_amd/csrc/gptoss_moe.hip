@@ -409,7 +409,8 @@ __device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x)
 
 // One wave: from the per-expert totals tot[0..E) (and dropped slots tot[E]),
 // write counts, exclusive offsets (global and offs[] in LDS) and the tile list
-// (kTileRows rows per tile) grouped by XCD.  An expert's tiles are cut into
+// (tr rows per tile: 32 for the LDS-staged GEMM, 64 for the direct one)
+// grouped by XCD.  An expert's tiles are cut into
 // units of up to 2 tiles; the U2 2-tile units are dealt to the 8 XCDs round
 // robin (unit rank r goes to XCD r % 8), then the U1 1-tile units continue the
 // deal.  That balances tiles per XCD within 2, and both tiles of a unit share
@@ -417,7 +418,7 @@ __device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x)
 // XCD x occupy tiles[xstart(x) .. xstart(x) + xcount(x)), 2-tile units first.
 __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ counts,
                             int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr,
-                            int E, int lane) {
+                            int E, int tr, int lane) {
     // lane l owns experts 4l .. 4l+3
     int c[4], nt[4], n2[4], n1[4];
     int csum = 0, s2 = 0, s1 = 0;
@@ -425,7 +426,7 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
     for (int j = 0; j < 4; ++j) {
         const int e = 4 * lane + j;
         c[j] = e < E ? tot[e] : 0;
-        nt[j] = (c[j] + kTileRows - 1) / kTileRows;
+        nt[j] = (c[j] + tr - 1) / tr;
         n2[j] = nt[j] / 2;
         n1[j] = nt[j] % 2;
         csum += c[j];
@@ -470,8 +471,8 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
                     if (xx == x) base = xstart[xx];
                 Tile tl;
                 tl.expert = e;
-                tl.row0 = off + m * kTileRows;
-                tl.rows = min(kTileRows, c[j] - m * kTileRows);
+                tl.row0 = off + m * tr;
+                tl.rows = min(tr, c[j] - m * tr);
                 tl.pad = 0;
                 tiles[base + pos] = tl;
             }
@@ -501,7 +502,8 @@ __global__ __launch_bounds__(1024) void plan_kernel(int32_t *__restrict__ hist, 
                                                    int32_t *__restrict__ counts,
                                                    int32_t *__restrict__ offsets,
                                                    int32_t *__restrict__ blkbase,
-                                                   Tile *__restrict__ tiles, int32_t *hdr) {
+                                                   Tile *__restrict__ tiles, int32_t *hdr,
+                                                   int tile_rows) {
     __shared__ int h[kMaxBlocks * kHistCols];
     __shared__ int tot[kHistCols];
     __shared__ int offs[kMaxExperts + 1];
@@ -533,7 +535,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(int32_t *__restrict__ hist, 
         tot[tid] = s;
     }
     __syncthreads();
-    if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tid);
+    if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tile_rows, tid);
     __syncthreads();
     for (int i = tid; i < n_blk * E; i += 1024) {
         const int b = i / E, e = i - b * E;
@@ -1419,6 +1421,460 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
     }
 }
 
+// ------------------------------------------------- packed weight layout --
+//
+// The direct decode GEMM reads weights that a one-time pack step
+// (gptoss_moe_pack_weights) rearranged into MFMA fragment order; byte values
+// are unchanged.  Per expert, for a matrix of N rows x K:
+//   nibbles: [ct < N/16][kp < KP = ceil(K/128)][lane 64][16 B].  Lane
+//            l = (n = l & 15, g = l >> 4) holds, for q = 0..3, the 4 bytes of
+//            packed row 16 ct + n at row byte 64 kp + 16 q + 4 g (k = 128 kp +
+//            32 q + 8 g .. + 7); zero past K.
+//   scales:  [ct][kc < KC = ceil(K/256)][16 rows][8 B]: e8m0 of packed row
+//            16 ct + n for k groups 8 kc .. 8 kc + 7; zero past K/32.
+// Packed row pr is weight row pr for MLP2.  For MLP1 each 32-row group puts
+// its 16 gate rows (even) in column tile 0 and its 16 up rows in tile 1, so
+// one lane's two accumulators hold gate and up of the same output column.
+struct PackLayout {
+    size_t w1, s1, w2, s2, total;
+};
+inline size_t pk_w_expert(int N, int K) { return (size_t)N * ((K + 127) / 128) * 64; }
+inline size_t pk_s_expert(int N, int K) { return (size_t)N * ((K + 255) / 256) * 8; }
+PackLayout pack_layout(const gptoss_moe_shape &s) {
+    const size_t E = (size_t)s.n_experts;
+    const int H = s.hidden, D = s.intermediate;
+    PackLayout L;
+    size_t o = 0;
+    auto take = [&](size_t b) {
+        size_t at = o;
+        o = align_up(o + b, 256);
+        return at;
+    };
+    L.w1 = take(E * pk_w_expert(2 * D, H));
+    L.s1 = take(E * pk_s_expert(2 * D, H));
+    L.w2 = take(E * pk_w_expert(H, D));
+    L.s2 = take(E * pk_s_expert(H, D));
+    L.total = o;
+    return L;
+}
+__device__ __forceinline__ int packed_src_row(int pr, bool mlp1) {
+    return mlp1 ? (pr & ~31) + 2 * (pr & 15) + ((pr >> 4) & 1) : pr;
+}
+// One thread per packed dword (nibbles) or byte (scales).
+__global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ wq,
+                                                  const uint8_t *__restrict__ ws, int N, int K,
+                                                  int E, int mlp1, uint32_t *__restrict__ pw,
+                                                  uint8_t *__restrict__ ps) {
+    const int KP = (K + 127) / 128, KC = (K + 255) / 256, CT = N / 16, KS = K / 32;
+    const size_t nw = (size_t)E * CT * KP * 256;  // dwords
+    const size_t nsb = (size_t)E * CT * KC * 128;  // bytes
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < nw + nsb;
+         i += (size_t)gridDim.x * 256) {
+        if (i < nw) {
+            const int q = (int)(i & 3), lane = (int)((i >> 2) & 63);
+            size_t r = i >> 8;
+            const int kp = (int)(r % KP);
+            r /= KP;
+            const int ct = (int)(r % CT);
+            const int e = (int)(r / CT);
+            const int row = packed_src_row(16 * ct + (lane & 15), mlp1 != 0);
+            const int byte = 64 * kp + 16 * q + 4 * (lane >> 4);
+            uint32_t v = 0;
+            if (byte < K / 2)
+                v = *reinterpret_cast<const uint32_t *>(wq + ((size_t)e * N + row) * (K / 2) + byte);
+            pw[i] = v;
+        } else {
+            const size_t b = i - nw;
+            const int gi = (int)(b & 7), n = (int)((b >> 3) & 15);
+            size_t r = b >> 7;
+            const int kc = (int)(r % KC);
+            r /= KC;
+            const int ct = (int)(r % CT);
+            const int e = (int)(r / CT);
+            const int row = packed_src_row(16 * ct + n, mlp1 != 0);
+            const int grp = 8 * kc + gi;
+            ps[b] = grp < KS ? ws[((size_t)e * N + row) * KS + grp] : (uint8_t)0;
+        }
+    }
+}
+
+// ------------------------------------------------- direct small-M GEMM --
+//
+// Decode path on packed weights.  One workgroup of 8 waves per CU (2 per
+// SIMD), persistent over (tile of up to 64 rows of one expert, block of 256
+// weight rows) items (ItemMap order); K is swept in stages of 256 k.  Tiles
+// of 64 rows cover a whole decode expert, so each weight block streams once,
+// and a 256-row block halves the activation bytes per weight byte.
+// Every wave w streams its 2 column tiles (weight rows 32 w .. 32 w + 31 of
+// the block) straight from the packed weights into MFMA fragment registers
+// (2 x 16 B per tile per stage, one coalesced 1 KB access per instruction),
+// kDDepth stages ahead; weights never pass through LDS.  The stage's
+// activations (64 x 256 bf16), e8m0 scales (2 KB), biases and token slots go
+// to LDS by direct global -> LDS loads one stage ahead, shared out over the
+// waves.  A wave dequantises one k step ahead of its MFMAs
+// (v_mfma_f32_16x16x32_bf16), activations and scales read from LDS.
+// A CU holds ~128 outstanding 1 KB loads before issue stalls; this schedule
+// keeps ~100 in flight, so no wave blocks in issue while it has MFMAs to run.
+// Iteration s: wait until only the last kDDepth - 1 weight stages are in
+// flight (so this wave's LDS loads of stage s have landed), barrier (every
+// wave's have; slot (s + 1) % 2 was last read in stage s - 1), issue the LDS
+// loads of stage s + 1, compute stage s, issue the weights of stage
+// s + kDDepth into the ring slot stage s used.
+// The barrier is a plain s_barrier: a workgroup fence there would also drain
+// the loads of later stages.
+// MFMA lane l = (n = l & 15, g = l >> 4): in k step ks of stage j, slot
+// (g, e) stands for k = 256 j + 32 ks + 8 g + e in both operands.
+constexpr int kDTileRows = 64;
+constexpr int kDBlockN = 256;
+constexpr int kDWaves = 8;
+constexpr int kDDepth = 2;  // weight stages in flight (registers)
+constexpr int kDSlots = 2;  // LDS stages: the one computed and the one loading
+constexpr int kDALoads = kDTileRows * kUnits / 64 / kDWaves;  // 1 KB activation loads per wave
+struct DSlot {
+    uint4 a[kDTileRows * kUnits];   // tile row r, 16-byte unit u at r * 32 + (u ^ (r & 15))
+    uint2 sc[kDBlockN];             // e8m0 of the stage: column tile c, row n at 16 c + n
+    uint16_t bias[kDBlockN];        // bias of block rows 0..255 (weight-row order)
+    int32_t slot[kDTileRows];       // token-order slot of tile row r (MLP2)
+};
+
+struct DArgs {
+    GemmArgs g;
+    const uint4 *pw;      // packed nibbles of this matrix
+    const uint2 *ps;      // packed scales
+};
+
+// s_waitcnt vmcnt(N), other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS reads of the slots the direct loads fill, issued as inline asm.  The
+// compiler cannot tell which in-flight global -> LDS load a read of a
+// dynamically chosen slot may alias, so for its own ds_read it drains every
+// outstanding global load (the later stages' weights included).  Here the
+// vmcnt wait + barrier protocol already orders the slot, and each result is
+// tied to an explicit lgkmcnt wait before use.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read_b128_at(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_wait(u32x4 &v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
+__device__ __forceinline__ void lds_wait(uint32_t &v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
+
+__device__ __forceinline__ uint2 lds_read_b64(uint32_t addr) {
+    uint2 v;
+    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_wait(uint2 &v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
+
+template <int MT>
+__device__ __forceinline__ void direct_stage(const DSlot &sl, const uint4 (&w)[2][2],
+                                             f32x4 (&acc)[4][2]) {
+    const int lane = threadIdx.x & 63, n_l = lane & 15, g = lane >> 4;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t abase = lds_addr(sl.a);
+    uint2 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) sc[t] = lds_read_b64(lds_addr(&sl.sc[16 * (2 * wave + t) + n_l]));
+#pragma unroll
+    for (int t = 0; t < 2; ++t) lds_wait(sc[t]);
+    auto deq = [&](int ks, int t) {
+        const uint32_t sw = ks < 4 ? sc[t].x : sc[t].y;
+        const uint32_t e = (sw >> (8 * (ks & 3))) & 0xffu;
+        // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
+        const uint32_t zm = e == 0 ? 0x88888888u : 0xffffffffu;
+        const uint4 v = w[t][ks >> 2];
+        const uint32_t dw = (ks & 3) == 0 ? v.x : (ks & 3) == 1 ? v.y : (ks & 3) == 2 ? v.z : v.w;
+        return dequant8(dw & zm, e8m0_to_f32(e));
+    };
+    // activation fragments of k step ks: row 16 m + n_l, unit (4 ks + g) ^ n_l
+    // = lane part 16 (n_l * 32 + (g ^ (n_l & 3))) + 64 (ks ^ (n_l >> 2)), and
+    // row group m at the immediate offset m * 32 rows * 512 B
+    const uint32_t alane = abase + 16u * (uint32_t)(n_l * kUnits + (g ^ (n_l & 3)));
+    auto areads = [&](int ks, u32x4 (&v)[MT]) {
+        const uint32_t ad = alane + 64u * (uint32_t)(ks ^ (n_l >> 2));
+        v[0] = lds_read_b128_at<0>(ad);
+        if constexpr (MT > 1) v[1] = lds_read_b128_at<16 * kUnits * 16>(ad);
+        if constexpr (MT > 2) v[2] = lds_read_b128_at<2 * 16 * kUnits * 16>(ad);
+        if constexpr (MT > 3) v[3] = lds_read_b128_at<3 * 16 * kUnits * 16>(ad);
+    };
+    u32x4 an[MT];
+    areads(0, an);
+    bf16x8 bn0 = deq(0, 0), bn1 = deq(0, 1);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const bf16x8 b0 = bn0, b1 = bn1;
+        bf16x8 af[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            lds_wait(an[m]);
+            af[m] = __builtin_bit_cast(bf16x8, an[m]);
+        }
+        if (ks < 7) {
+            areads(ks + 1, an);
+            bn0 = deq(ks + 1, 0);
+            bn1 = deq(ks + 1, 1);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], b0, acc[m][0], 0, 0, 0);
+            acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], b1, acc[m][1], 0, 0, 0);
+        }
+    }
+}
+
+template <int MT, bool kMlp1>
+__device__ __forceinline__ void direct_epilogue(const GemmArgs &a, const DSlot &sl, const Tile &tl,
+                                                int nb, const f32x4 (&acc)[4][2]) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, n_l = lane & 15, g = lane >> 4;
+    const int N = a.N;
+    const int wcol0 = nb * kDBlockN + 32 * w;
+    if (wcol0 >= N) return;
+    if (kMlp1) {
+        const int D = N / 2;
+        const int jc = wcol0 / 2 + n_l;
+        uint32_t gu = lds_read_b32(lds_addr(&sl.bias[32 * w + 2 * n_l]));  // gate, up bias pair
+        lds_wait(gu);
+        const float bg = __uint_as_float(gu << 16);
+        const float bu = __uint_as_float(gu & 0xffff0000u);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * m + 4 * g + v;
+                if (r < tl.rows) {
+                    float gt = bf16_round(acc[m][0][v] + bg);
+                    float up = bf16_round(acc[m][1][v] + bu);
+                    gt = fminf(fmaxf(gt, -a.limit), a.limit);
+                    up = fminf(fmaxf(up, -a.limit), a.limit);
+                    const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
+                    gt = gt * sig;
+                    a.out_act[(size_t)(tl.row0 + r) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                }
+            }
+    } else {
+        // bias of columns wcol0 + n_l and + 16 (low / high half of an aligned pair)
+        uint32_t b0 = lds_read_b32(lds_addr(&sl.bias[(32 * w + n_l) & ~1]));
+        uint32_t b1 = lds_read_b32(lds_addr(&sl.bias[(32 * w + 16 + n_l) & ~1]));
+        uint32_t sv[MT][4];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                sv[m][v] = lds_read_b32(lds_addr(&sl.slot[16 * m + 4 * g + v]));
+        lds_wait(b0);
+        lds_wait(b1);
+        float bb[2];
+        bb[0] = __uint_as_float((n_l & 1) ? (b0 & 0xffff0000u) : (b0 << 16));
+        bb[1] = __uint_as_float((n_l & 1) ? (b1 & 0xffff0000u) : (b1 << 16));
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                lds_wait(sv[m][v]);
+                const int r = 16 * m + 4 * g + v;
+                if (r < tl.rows) {
+                    uint16_t *dst = a.out_slots + (size_t)sv[m][v] * N + wcol0 + n_l;
+                    dst[0] = f2bf(acc[m][0][v] + bb[0]);
+                    dst[16] = f2bf(acc[m][1][v] + bb[1]);
+                }
+            }
+    }
+}
+
+template <bool kMlp1>
+__global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
+    __shared__ DSlot slots[kDSlots];
+    const GemmArgs &a = d.g;
+    ItemMap im;
+    int n_items;
+    im.init(a.hdr, (a.N + kDBlockN - 1) / kDBlockN, n_items);
+    const int NST = (a.K + kStageK - 1) / kStageK;
+    if (n_items == 0) return;
+    const int total = n_items * NST;
+    const int total_p = (total + kDDepth - 1) / kDDepth * kDDepth;
+    // wave index uniform for the compiler too: LDS destinations must be scalar
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int N = a.N, K = a.K;
+    const int CT = N / 16, KP = (K + 127) / 128, KC = (K + 255) / 256;
+    uint4 wr[kDDepth][2][2];
+    StepCursor wcur, lcur, ccur;
+    wcur.init(a, im, n_items);
+    lcur.init(a, im, n_items);
+    ccur.init(a, im, n_items);
+
+    // Weights of stage st (2 column tiles x 2 x 16 B per lane) into ring slot r.
+    auto issue_w = [&](int st, int r) {
+        st = min(st, total - 1);
+        Tile tl;
+        int nb, j;
+        wcur.at(a, im, NST, st, tl, nb, j);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int ct = min(nb * (kDBlockN / 16) + 2 * w + t, CT - 1);  // past N: unused data
+            const size_t tile = (size_t)tl.expert * CT + ct;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                wr[r][t][h] = d.pw[(tile * KP + min(2 * j + h, KP - 1)) * 64 + lane];
+        }
+    };
+    // Direct global -> LDS loads of stage st into slot st % kDSlots.  Only
+    // the waves that own a piece load it, and activation row pairs no MFMA
+    // reads are skipped, so their number varies; the waits do not count on it.
+    auto issue_lds = [&](int st) {
+        DSlot &sl = slots[st % kDSlots];
+        st = min(st, total - 1);
+        Tile tl;
+        int nb, j;
+        lcur.at(a, im, NST, st, tl, nb, j);
+        // activations: load i of wave w fills LDS units 64 q .. 64 q + 63,
+        // q = kDALoads w + i (tile rows 2 q, 2 q + 1); lane l fetches the unit
+        // its LDS position stands for under the row swizzle.  Rows past the
+        // tile repeat its last row, k past K the last unit (against zero
+        // weights).
+        const char *base = reinterpret_cast<const char *>(a.A + (size_t)tl.row0 * K);
+        const int rmax = tl.rows - 1;
+        const int rpad = (tl.rows + 15) & ~15;  // rows the MFMAs read
+#pragma unroll
+        for (int i = 0; i < kDALoads; ++i) {
+            const int q = kDALoads * w + i;
+            if (2 * q < rpad) {
+                const int x = 64 * q + lane;
+                const int rr = x >> 5, u = (x & 31) ^ (rr & 15);
+                const uint32_t off = (uint32_t)min(rr, rmax) * (2u * K) +
+                                     2u * (uint32_t)min(j * kStageK + 8 * u, K - 8);
+                __builtin_amdgcn_global_load_lds(base + off, &sl.a[64 * q], 16, 0, 0);
+            }
+        }
+        // LDS destinations as element addresses: an array argument is not
+        // decayed to a pointer by this builtin
+        if (w < 2) {
+            // scales: 16 column tiles x 128 B; wave w loads tiles 8 w .. 8 w + 7
+            // (lane l: tile 8 w + (l >> 3), 16-byte part l & 7)
+            const int ct = min(nb * (kDBlockN / 16) + 8 * w + (lane >> 3), CT - 1);
+            const char *src = reinterpret_cast<const char *>(d.ps) +
+                              ((((size_t)tl.expert * CT + ct) * KC + j) * 128 + 16 * (lane & 7));
+            __builtin_amdgcn_global_load_lds(src, &sl.sc[128 * w], 16, 0, 0);
+        } else if (w < 4) {
+            // biases of block rows 128 (w - 2) .. + 127, 2 per lane
+            const int h = w - 2;
+            __builtin_amdgcn_global_load_lds(
+                a.bias + (size_t)tl.expert * N + min(nb * kDBlockN + 128 * h + 2 * lane, N - 2),
+                &sl.bias[128 * h], 4, 0, 0);
+        } else if (w == 4) {
+            __builtin_amdgcn_global_load_lds(a.row_slot + tl.row0 + min(lane, rmax), &sl.slot[0],
+                                             4, 0, 0);
+        }
+    };
+
+#ifdef GPTOSS_TRACE
+    unsigned long long tw = 0, tb = 0, tc = 0, te = 0, ti = 0, tq;
+    const unsigned long long tstart = __builtin_readcyclecounter();
+#define DTR(var) (var) += __builtin_readcyclecounter() - tq; tq = __builtin_readcyclecounter();
+#else
+#define DTR(var)
+#endif
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // issue order: lds(0), w(0), w(1); then per iteration s: lds(s + 1), w(s + 2)
+    issue_lds(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < kDDepth; ++r) {
+        issue_w(r, r);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#ifdef GPTOSS_TRACE
+    tq = __builtin_readcyclecounter();
+#endif
+    for (int s0 = 0; s0 < total_p; s0 += kDDepth) {
+#pragma unroll
+        for (int r = 0; r < kDDepth; ++r) {
+            const int s = s0 + r;
+            __builtin_amdgcn_sched_barrier(0);
+            // behind stage s's LDS loads only weight loads were issued: the
+            // last kDDepth - 1 stages' (4 each) may stay in flight
+            wait_vmcnt<4 * (kDDepth - 1)>();
+            DTR(tw)
+            __builtin_amdgcn_s_barrier();  // everyone's loads of stage s landed; slot (s+1) % 2 is free
+            __builtin_amdgcn_sched_barrier(0);
+            DTR(tb)
+            // the next stage's LDS loads first, so the memory pipeline works
+            // through them while the MFMAs run
+            issue_lds(s + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            DTR(ti)
+            if (s < total) {
+                Tile tl;
+                int nb, j;
+                ccur.at(a, im, NST, s, tl, nb, j);
+                uint4(&wv)[2][2] = wr[r];
+                // k groups of a stage past K: kp >= KP is a clamped reload, zero it
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t km = -(uint32_t)(2 * j + h < KP);
+                        wv[t][h] = make_uint4(wv[t][h].x & km, wv[t][h].y & km, wv[t][h].z & km,
+                                              wv[t][h].w & km);
+                    }
+                const DSlot &sl = slots[s % kDSlots];
+                const int mt = (tl.rows + 15) >> 4;
+                if (mt <= 1) direct_stage<1>(sl, wv, acc);
+                else if (mt == 2) direct_stage<2>(sl, wv, acc);
+                else if (mt == 3) direct_stage<3>(sl, wv, acc);
+                else direct_stage<4>(sl, wv, acc);
+                DTR(tc)
+                if (j == NST - 1) {
+                    if (mt <= 1) direct_epilogue<1, kMlp1>(a, sl, tl, nb, acc);
+                    else if (mt == 2) direct_epilogue<2, kMlp1>(a, sl, tl, nb, acc);
+                    else if (mt == 3) direct_epilogue<3, kMlp1>(a, sl, tl, nb, acc);
+                    else direct_epilogue<4, kMlp1>(a, sl, tl, nb, acc);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    DTR(te)
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            issue_w(s + kDDepth, r);
+        }
+    }
+    wait_vmcnt<0>();  // no LDS write in flight when the workgroup ends
+#ifdef GPTOSS_TRACE
+    if (lane == 0) {  // vector atomics from one lane: per-wave cycle totals
+        unsigned long long *t = reinterpret_cast<unsigned long long *>(const_cast<int32_t *>(a.hdr) + 128) + (kMlp1 ? 0 : 32);
+        atomicAdd(t + 0, tw);
+        atomicAdd(t + 1, tb);
+        atomicAdd(t + 2, tc);
+        atomicAdd(t + 3, te);
+        atomicAdd(t + 4, ti);
+        atomicAdd(t + 5, __builtin_readcyclecounter() - tstart);
+        atomicAdd(t + 6, (unsigned long long)total);
+    }
+#endif
+#undef DTR
+}
+
 // Weighted top-k reduction (reduce_tokenwise_expert_outputs_bf16_bf16wts,
 // moe.hpp:700-730): e_agg[t][h] = bf16(sum over live slots j, in slot order,
 // of fmaf(w[t][j], y[t][j][h], acc)); with residual, out = bf16(out + e_agg)
@@ -1643,7 +2099,7 @@ void launch_route_tb(int ee, const gptoss_moe_shape *s, const gptoss_moe_weights
 
 int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                  int T, const int32_t *fi, const uint16_t *fw, const Ptrs &p, hipStream_t st,
-                 Marks *mk = nullptr) {
+                 int tile_rows, Marks *mk = nullptr) {
     int nthreads_ref = 1;
     while (nthreads_ref < s->n_experts) nthreads_ref <<= 1;
     nthreads_ref = nthreads_ref < 64 ? 64 : (nthreads_ref > 512 ? 512 : nthreads_ref);
@@ -1665,7 +2121,7 @@ int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const u
     else
         launch_route_tb<1>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, p.hist, n_blk, E, p.counts,
-                       p.offsets, p.blkbase, p.tiles, p.hdr);
+                       p.offsets, p.blkbase, p.tiles, p.hdr, tile_rows);
     if (mk) mk->mark(st);
     int G = 8 * device_cus() / n_blk;
     G = G < 1 ? 1 : (G > 256 ? 256 : G);
@@ -1686,6 +2142,32 @@ bool use_large_m(const gptoss_moe_shape *s, int T, unsigned flags) {
     if (!fits || (flags & GPTOSS_MOE_FLAG_SMALL_M_GEMM)) return false;
     if (flags & GPTOSS_MOE_FLAG_LARGE_M_GEMM) return true;
     return P >= 96L * s->n_experts;
+}
+
+// GEMM path of a forward call.  With packed weights the direct GEMM runs at
+// every batch size (it outruns the large-M path on prefill too) unless a
+// flag forces another path; without them the small-M / large-M choice above.
+enum GemmPath { PATH_SMALL_M, PATH_LARGE_M, PATH_DIRECT };
+GemmPath gemm_path(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, unsigned flags) {
+    if (flags & GPTOSS_MOE_FLAG_LARGE_M_GEMM) return use_large_m(s, T, flags) ? PATH_LARGE_M : PATH_SMALL_M;
+    if (w->packed != nullptr && !(flags & GPTOSS_MOE_FLAG_SMALL_M_GEMM)) return PATH_DIRECT;
+    return use_large_m(s, T, flags) ? PATH_LARGE_M : PATH_SMALL_M;
+}
+
+// Rows per tile of the tile list: the direct GEMM takes whole decode experts,
+// up to 64 rows; the LDS-staged GEMM 32 (the large-M GEMM builds its own).
+int gemm_tile_rows(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, unsigned flags) {
+    return gemm_path(s, w, T, flags) == PATH_DIRECT ? kDTileRows : kTileRows;
+}
+
+// Expert weights and flags of a forward call.
+int check_experts(const gptoss_moe_weights *w, unsigned flags) {
+    if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (!w->w1 || !w->w1_scales || !w->b1 || !w->w2 || !w->w2_scales || !w->b2)
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (!aligned16(w->w1) || !aligned16(w->w2) || !aligned16(w->packed))
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    return GPTOSS_MOE_OK;
 }
 
 int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
@@ -1709,10 +2191,16 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a1.K = H;
     a1.limit = s->swiglu_limit;
     a1.alpha = s->swiglu_alpha;
-    const bool large = use_large_m(s, T, flags);
+    const GemmPath path = gemm_path(s, w, T, flags);
+    const bool large = path == PATH_LARGE_M, direct = path == PATH_DIRECT;
+    const PackLayout PL = pack_layout(*s);
     if (large)
         hipLaunchKernelGGL(large_m_gemm_kernel<true>, dim3(cap), dim3(kLWaves * 64), 0, st, a1,
                            p.counts, p.offsets, s->n_experts);
+    else if (direct)
+        hipLaunchKernelGGL(direct_gemm_kernel<true>, dim3(cap), dim3(kDWaves * 64), 0, st,
+                           DArgs{a1, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
+                                 reinterpret_cast<const uint2 *>(w->packed + PL.s1)});
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a1);
     if (mk) mk->mark(st);
@@ -1729,6 +2217,10 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     if (large)
         hipLaunchKernelGGL(large_m_gemm_kernel<false>, dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                            p.counts, p.offsets, s->n_experts);
+    else if (direct)
+        hipLaunchKernelGGL(direct_gemm_kernel<false>, dim3(cap), dim3(kDWaves * 64), 0, st,
+                           DArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
+                                 reinterpret_cast<const uint2 *>(w->packed + PL.s2)});
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a2);
     if (mk) mk->mark(st);
@@ -1791,7 +2283,7 @@ int gptoss_moe_route(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
     if (!x_norm || !aligned16(x_norm)) return GPTOSS_MOE_ERR_INVALID_ARG;
     const WsLayout L = ws_layout(*shape, max_tokens);
     return launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w,
-                        ws_ptrs(L, workspace), stream);
+                        ws_ptrs(L, workspace), stream, gemm_tile_rows(shape, w, n_tokens, 0));
 }
 
 int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
@@ -1802,15 +2294,13 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     int rc = check_common(shape, w, n_tokens, forced_topk_i, forced_topk_w, workspace, ws_bytes,
                           max_tokens);
     if (rc) return rc;
-    if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (!w->w1 || !w->w1_scales || !w->b1 || !w->w2 || !w->w2_scales || !w->b2)
-        return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (!aligned16(w->w1) || !aligned16(w->w2)) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if ((rc = check_experts(w, flags)) != 0) return rc;
     if (n_tokens == 0) return GPTOSS_MOE_OK;
     if (!x_norm || !out || !aligned16(x_norm) || !aligned16(out)) return GPTOSS_MOE_ERR_INVALID_ARG;
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
-    rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream);
+    rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
+                      gemm_tile_rows(shape, w, n_tokens, flags));
     if (rc) return rc;
     return launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream);
 }
@@ -1823,8 +2313,9 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
     int rc = check_common(shape, w, n_tokens, forced_topk_i, forced_topk_w, workspace, ws_bytes,
                           max_tokens);
     if (rc) return rc;
+    if ((rc = check_experts(w, flags)) != 0) return rc;
     if (!kernel_ms || n_tokens == 0 || !x_norm || !out) return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (!aligned16(x_norm) || !aligned16(out)) return GPTOSS_MOE_ERR_INVALID_ARG;
     Marks mk;
     mk.on = true;
     for (int i = 0; i < 6; ++i)
@@ -1832,7 +2323,8 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
     mk.mark(stream);
-    rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream, &mk);
+    rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
+                      gemm_tile_rows(shape, w, n_tokens, flags), &mk);
     if (!rc) rc = launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream, &mk);
     if (!rc) rc = hip_status(hipEventSynchronize(mk.ev[5]));
     for (int i = 0; i < 5 && !rc; ++i)
@@ -1873,6 +2365,31 @@ int gptoss_moe_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int n
     if (blocks > 1024) blocks = 1024;
     hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks, n_experts), dim3(256), 0, stream,
                        packed, scales, seg, out);
+    return hip_status(hipGetLastError());
+}
+
+size_t gptoss_moe_packed_size(const gptoss_moe_shape *shape) {
+    if (!shape_ok(shape)) return 0;
+    return pack_layout(*shape).total;
+}
+
+int gptoss_moe_pack_weights(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                            void *packed, size_t bytes, hipStream_t stream) {
+    if (!shape_ok(shape) || !w || !w->w1 || !w->w1_scales || !w->w2 || !w->w2_scales || !packed)
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (shape->hidden > kMaxHidden || shape->intermediate > kMaxHidden)
+        return GPTOSS_MOE_ERR_UNSUPPORTED;
+    if (!aligned16(w->w1) || !aligned16(w->w2) || !aligned16(packed))
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    const PackLayout L = pack_layout(*shape);
+    if (bytes < L.total) return GPTOSS_MOE_ERR_WORKSPACE;
+    uint8_t *pb = static_cast<uint8_t *>(packed);
+    const int H = shape->hidden, D = shape->intermediate, E = shape->n_experts;
+    const int grid = 4 * device_cus();
+    hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(256), 0, stream, w->w1, w->w1_scales, 2 * D, H,
+                       E, 1, reinterpret_cast<uint32_t *>(pb + L.w1), pb + L.s1);
+    hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(256), 0, stream, w->w2, w->w2_scales, H, D, E,
+                       0, reinterpret_cast<uint32_t *>(pb + L.w2), pb + L.s2);
     return hip_status(hipGetLastError());
 }
 

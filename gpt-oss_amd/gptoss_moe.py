@@ -49,7 +49,8 @@ class Shape(ctypes.Structure):
 
 class Weights(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
-                ("router_w", "router_b", "w1", "w1_scales", "b1", "w2", "w2_scales", "b2")]
+                ("router_w", "router_b", "w1", "w1_scales", "b1", "w2", "w2_scales", "b2",
+                 "packed")]
 
 
 class Views(ctypes.Structure):
@@ -81,6 +82,9 @@ _SIGS = {
     "gptoss_moe_rmsnorm": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
     "gptoss_moe_dequant_mxfp4": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int64,
                                                 ctypes.c_int64, _VP, _VP]),
+    "gptoss_moe_packed_size": (ctypes.c_size_t, [ctypes.POINTER(Shape)]),
+    "gptoss_moe_pack_weights": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights),
+                                               _VP, ctypes.c_size_t, _VP]),
     "gptoss_moe_last_hip_error": (ctypes.c_int, []),
     "gptoss_moe_version": (ctypes.c_char_p, []),
 }
@@ -134,14 +138,18 @@ class MoeLayer:
     include/gptoss_moe.h.  `max_tokens` sizes the workspace.
     """
 
-    def __init__(self, shape: Shape, weights: dict, max_tokens: int, device="cuda"):
+    def __init__(self, shape: Shape, weights: dict, max_tokens: int, device="cuda",
+                 pack: bool = True):
         import torch
         self.lib = load_library()
         self.shape = shape
         self.max_tokens = int(max_tokens)
         self.device = torch.device(device)
         self.tensors = dict(weights)  # keep device buffers alive
+        self.tensors.pop("packed", None)
         self.w = Weights(*[_ptr(self.tensors.get(n)) for n, _ in Weights._fields_])
+        if pack:
+            self.pack()
         self.ws_bytes = workspace_size(shape, self.max_tokens)
         if self.ws_bytes == 0:
             raise MoeError("gptoss_moe_workspace_size", ERR_INVALID_ARG)
@@ -149,8 +157,28 @@ class MoeLayer:
         _check("gptoss_moe_workspace_init",
                self.lib.gptoss_moe_workspace_init(self.ws.data_ptr(), self.ws_bytes, _stream()))
 
+    def pack(self):
+        """Build the MFMA-ordered copy of w1/w2 (gptoss_moe_pack_weights) and use it."""
+        import torch
+        n = int(self.lib.gptoss_moe_packed_size(ctypes.byref(self.shape)))
+        if n == 0:
+            raise MoeError("gptoss_moe_packed_size", ERR_INVALID_ARG)
+        self.w.packed = None
+        buf = torch.empty(n, dtype=torch.uint8, device=self.device)
+        _check("gptoss_moe_pack_weights",
+               self.lib.gptoss_moe_pack_weights(ctypes.byref(self.shape), ctypes.byref(self.w),
+                                                buf.data_ptr(), n, _stream()))
+        self.tensors["packed"] = buf
+        self.w.packed = buf.data_ptr()
+
+    def unpack(self):
+        """Drop the packed copy: later calls read w1/w2 directly."""
+        self.tensors.pop("packed", None)
+        self.w.packed = None
+
     @classmethod
-    def from_numpy(cls, d, max_tokens: Optional[int] = None, device="cuda") -> "MoeLayer":
+    def from_numpy(cls, d, max_tokens: Optional[int] = None, device="cuda",
+                   pack: bool = True) -> "MoeLayer":
         """Upload a synth.MoeData layer."""
         import torch
         c = d.cfg
@@ -166,7 +194,7 @@ class MoeLayer:
              "w1_scales": up(d.s1), "b1": up(d.b1), "w2": up(d.w2), "w2_scales": up(d.s2),
              "b2": up(d.b2)}
         shape = make_shape(c.hidden, c.intermediate, c.n_experts, c.top_k)
-        return cls(shape, w, max_tokens or c.tokens, device)
+        return cls(shape, w, max_tokens or c.tokens, device, pack=pack)
 
     # -- entry points ---------------------------------------------------
     def forward(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,

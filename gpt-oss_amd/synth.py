@@ -48,6 +48,8 @@ CONFIGS = {
     "c3b_120b_prefill": MoeConfig("c3b_120b_prefill", 2880, 2880, 128, 4, 4096, "router", 0x6F550004),
     # test-only: many rows per expert at a small shape (large-M GEMM path, ragged tiles)
     "t_large_m": MoeConfig("t_large_m", 384, 320, 6, 2, 700, "router", 0x6F550010),
+    # test-only: H = 1.5 weight blocks of 128 rows, D = 3.5 packed k groups of 128
+    "t_odd_n": MoeConfig("t_odd_n", 192, 448, 5, 2, 40, "router", 0x6F550011),
 }
 
 

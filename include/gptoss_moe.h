@@ -42,9 +42,11 @@ extern "C" {
 #define GPTOSS_MOE_FLAG_RESIDUAL_ADD 1u
 /* GEMM path selection (no counterpart in the reference, which picks its tile
  * shape from the largest expert count, getp_run.cpp:2666).  By default the
- * large-M path (128-row tiles) runs when experts average >= 96 rows; these
- * force either path.  The large-M path needs hidden, intermediate >= 256 and
- * falls back to the small-M path otherwise. */
+ * direct GEMM runs when weights.packed is set (any batch size); without it
+ * the large-M GEMM (128-row tiles) runs when experts average >= 96 rows and
+ * the LDS-staged small-M GEMM otherwise.  SMALL_M forces the LDS-staged
+ * small-M GEMM, LARGE_M the large-M GEMM (which needs hidden, intermediate
+ * >= 256 and falls back to small-M otherwise). */
 #define GPTOSS_MOE_FLAG_SMALL_M_GEMM 2u
 #define GPTOSS_MOE_FLAG_LARGE_M_GEMM 4u
 
@@ -69,6 +71,10 @@ typedef struct gptoss_moe_weights {
     const uint8_t *w2;         /* MXFP4 nibbles, E * (H*D/2) bytes */
     const uint8_t *w2_scales;  /* e8m0, E * (H*D/32) bytes */
     const uint16_t *b2;        /* bf16 [E][H] */
+    const uint8_t *packed;     /* optional: w1/w2 and their scales rearranged by
+                                * gptoss_moe_pack_weights (NULL = not packed).
+                                * When set, small batches run the direct GEMM
+                                * on it; w1/w2 are still read by large ones. */
 } gptoss_moe_weights;
 
 /* Views into a workspace after a call, for inspection and parity tests.
@@ -164,6 +170,19 @@ int gptoss_moe_rmsnorm(const uint16_t *x, const uint16_t *weight, uint16_t *out,
 int gptoss_moe_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int n_experts,
                              int64_t n_rows, int64_t k_cols, uint16_t *out,
                              hipStream_t stream);
+
+/*
+ * Load-time weight packing (no counterpart in the reference, whose loader
+ * converts weights once at start-up, getp_run.cpp:1041-1049): rearranges the
+ * MXFP4 nibbles and e8m0 scales of w1 and w2 into MFMA fragment order for the
+ * direct decode GEMM; byte values are unchanged, K is padded to a multiple of
+ * 128 with zeros.  Run once per layer, keep the buffer and pass it as
+ * weights.packed.  gptoss_moe_packed_size gives the buffer size (0 for an
+ * invalid shape); the buffer must be 16-byte aligned.
+ */
+size_t gptoss_moe_packed_size(const gptoss_moe_shape *shape);
+int gptoss_moe_pack_weights(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                            void *packed, size_t bytes, hipStream_t stream);
 
 /* Last HIP error seen by this library on the calling thread (hipError_t). */
 int gptoss_moe_last_hip_error(void);

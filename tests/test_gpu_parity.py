@@ -127,10 +127,10 @@ def test_routing_invalid_and_duplicate_slots(gpu):
 
 
 # ---------------------------------------------------------------- forward --
-def _forward(d, gpu, rows_check=None, residual=False, path="auto"):
+def _forward(d, gpu, rows_check=None, residual=False, path="auto", pack=True):
     import gptoss_moe
     c = d.cfg
-    layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
+    layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu, pack=pack)
     x = _dev(d.x, gpu)
     fi = None if d.forced_i is None else _dev(d.forced_i, gpu)
     fw = None if d.forced_w is None else _dev(d.forced_w, gpu)
@@ -164,6 +164,62 @@ def test_forward_gemm_paths(gpu, name, path):
     d = _data(name)
     _, _, _, m = _forward(d, gpu, path=path)
     print(name, path, m)
+
+
+@pytest.mark.parametrize("name", ["c0_tiny", "t_large_m", "t_odd_n", "c1_20b_decode"])
+def test_forward_small_m_unpacked(gpu, name):
+    """The LDS-staged small-M GEMM on the original weight layout (no packed copy)."""
+    d = _data(name)
+    _, _, _, m = _forward(d, gpu, path="small", pack=False)
+    print(name, m)
+
+
+@pytest.mark.parametrize("name", ["t_odd_n", "t_large_m"])
+def test_forward_direct_ragged(gpu, name):
+    """The direct GEMM on packed weights where N is not a multiple of the
+    256-row weight block and K not a multiple of the 256-k stage, and (t_large_m)
+    experts of several 64-row tiles."""
+    d = _data(name)
+    _, _, _, m = _forward(d, gpu)
+    print(name, m)
+
+
+def _pack_expected(wq, ws, n, k, mlp1):
+    """Packed nibbles and scales of one matrix [E][n][k] laid out as the
+    direct GEMM reads them: nibbles [E][n/16][kp][g][16 rows][q][4 B] with
+    byte 64 kp + 16 q + 4 g of the row, scales [E][n/16][kc][16 rows][8]."""
+    e = wq.shape[0] // (n * k // 2)
+    kp, kc, ks = -(-k // 128), -(-k // 256), k // 32
+    pr = np.arange(n)
+    src = ((pr & ~31) + 2 * (pr & 15) + ((pr >> 4) & 1)) if mlp1 else pr
+    w = np.zeros((e, n, kp * 64), np.uint8)
+    w[:, :, :k // 2] = wq.reshape(e, n, k // 2)[:, src]
+    w = w.reshape(e, n // 16, 16, kp, 4, 4, 4).transpose(0, 1, 3, 5, 2, 4, 6)
+    s = np.zeros((e, n, kc * 8), np.uint8)
+    s[:, :, :ks] = ws.reshape(e, n, ks)[:, src]
+    s = s.reshape(e, n // 16, 16, kc, 8).transpose(0, 1, 3, 2, 4)
+    return w.reshape(-1), s.reshape(-1)
+
+
+@pytest.mark.parametrize("name", ["c0_tiny", "t_odd_n"])
+def test_pack_layout_bit_exact(gpu, name):
+    """gptoss_moe_pack_weights moves bytes only: its output equals a numpy
+    permutation of the MXFP4 nibbles and scales, with zero padding past K."""
+    import gptoss_moe
+    d = _data(name)
+    c = d.cfg
+    layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
+    got = layer.tensors["packed"].cpu().numpy()
+    H, D = c.hidden, c.intermediate
+    o = 0
+    for wq, ws, n, k, mlp1 in ((d.w1, d.s1, 2 * D, H, True), (d.w2, d.s2, H, D, False)):
+        ew, es = _pack_expected(np.ascontiguousarray(wq).reshape(-1),
+                                np.ascontiguousarray(ws).reshape(-1), n, k, mlp1)
+        assert np.array_equal(got[o:o + ew.size], ew), "nibbles"
+        o = -(-(o + ew.size) // 256) * 256
+        assert np.array_equal(got[o:o + es.size], es), "scales"
+        o = -(-(o + es.size) // 256) * 256
+    assert o == got.size
 
 
 def test_forward_120b_prefill_sampled(gpu):
