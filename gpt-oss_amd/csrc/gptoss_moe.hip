@@ -1718,6 +1718,10 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     const int CT = N / 16, KP = (K + 127) / 128, KC = (K + 255) / 256;
     uint4 wr[kDDepth][2][2];
     StepCursor wcur, lcur, ccur;
+#ifdef GPTOSS_TRACE
+    int lds_count = 0;  // this wave's LDS loads of the last issued stage
+    unsigned long long twl = 0;
+#endif
     wcur.init(a, im, n_items);
     lcur.init(a, im, n_items);
     ccur.init(a, im, n_items);
@@ -1746,6 +1750,9 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
         Tile tl;
         int nb, j;
         lcur.at(a, im, NST, st, tl, nb, j);
+#ifdef GPTOSS_TRACE
+        lds_count = min(max(((tl.rows + 15) & ~15) / 2 - kDALoads * w, 0), kDALoads) + (w < 5 ? 1 : 0);
+#endif
         // activations: load i of wave w fills LDS units 64 q .. 64 q + 63,
         // q = kDALoads w + i (tile rows 2 q, 2 q + 1); lane l fetches the unit
         // its LDS position stands for under the row swizzle.  Rows past the
@@ -1814,8 +1821,20 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
             __builtin_amdgcn_sched_barrier(0);
             // behind stage s's LDS loads only weight loads were issued: the
             // last kDDepth - 1 stages' (4 each) may stay in flight
-            wait_vmcnt<4 * (kDDepth - 1)>();
+#ifdef GPTOSS_TRACE
+            // weights of stage s only (issued before stage s's LDS loads)
+            switch (lds_count) {
+            case 0: wait_vmcnt<4>(); break;
+            case 1: wait_vmcnt<5>(); break;
+            case 2: wait_vmcnt<6>(); break;
+            case 3: wait_vmcnt<7>(); break;
+            case 4: wait_vmcnt<8>(); break;
+            default: wait_vmcnt<9>(); break;
+            }
             DTR(tw)
+#endif
+            wait_vmcnt<4 * (kDDepth - 1)>();
+            DTR(twl)
             __builtin_amdgcn_s_barrier();  // everyone's loads of stage s landed; slot (s+1) % 2 is free
             __builtin_amdgcn_sched_barrier(0);
             DTR(tb)
@@ -1870,9 +1889,63 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
         atomicAdd(t + 4, ti);
         atomicAdd(t + 5, __builtin_readcyclecounter() - tstart);
         atomicAdd(t + 6, (unsigned long long)total);
+        atomicAdd(t + 7, twl);
     }
 #endif
 #undef DTR
+}
+
+// fp32 -> MXFP4 (quantize_pack_mxfp4_block32_kernel, mxfp4.hpp:112-217), the
+// load-time quantiser of the reference's weight loader.  One 32-lane half of
+// a wave per 32-element block of the flattened array (tail zero-filled):
+// maxabs by butterfly (NaN never wins, as the reference's `a > maxabs`),
+// exp = ilogb(maxabs) - 2 via frexpf (0 for an all-zero block), scale byte
+// clamp(exp + 127, 0, 255), code = the nearest of the 16 E2M1 values to
+// v / 2^exp by the reference's brute-force scan (strict <: ties to the lower
+// code index), two codes per byte, low nibble = even element.
+__constant__ float kE2M1Lut[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                   -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+__global__ __launch_bounds__(256) void quantize_mxfp4_kernel(const float *__restrict__ src, int64_t n,
+                                                            int64_t nblocks,
+                                                            uint8_t *__restrict__ packed,
+                                                            uint8_t *__restrict__ scales) {
+    const int lane = threadIdx.x & 31;
+    for (int64_t blk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5; blk < nblocks;
+         blk += (int64_t)gridDim.x * 8) {  // uniform per 32 lanes
+        const int64_t i = blk * 32 + lane;
+        const float v = i < n ? src[i] : 0.0f;
+        const float av = fabsf(v);
+        float m = av > 0.0f ? av : 0.0f;  // NaN -> 0
+#pragma unroll
+        for (int s = 16; s >= 1; s >>= 1) {
+            const float o = __shfl_xor(m, s, 32);
+            m = o > m ? o : m;
+        }
+        int exp_scale = 0;
+        if (m > 0.0f) {
+            int e;
+            frexpf(m, &e);
+            exp_scale = (e - 1) - 2;
+        }
+        const float X = ldexpf(1.0f, exp_scale);
+        const float x = v / X;
+        int best = 0;
+        float best_diff = fabsf(x - kE2M1Lut[0]);
+#pragma unroll
+        for (int c = 1; c < 16; ++c) {
+            const float dd = fabsf(x - kE2M1Lut[c]);
+            if (dd < best_diff) {
+                best_diff = dd;
+                best = c;
+            }
+        }
+        const int hi = __shfl_down(best, 1, 32);
+        if ((lane & 1) == 0) packed[blk * 16 + (lane >> 1)] = (uint8_t)((hi << 4) | best);
+        if (lane == 0) {
+            const int eb = exp_scale + 127;
+            scales[blk] = (uint8_t)(eb < 0 ? 0 : (eb > 255 ? 255 : eb));
+        }
+    }
 }
 
 // Weighted top-k reduction (reduce_tokenwise_expert_outputs_bf16_bf16wts,
@@ -2365,6 +2438,19 @@ int gptoss_moe_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int n
     if (blocks > 1024) blocks = 1024;
     hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks, n_experts), dim3(256), 0, stream,
                        packed, scales, seg, out);
+    return hip_status(hipGetLastError());
+}
+
+int gptoss_moe_quantize_mxfp4(const float *src, int64_t n_elems, uint8_t *packed, uint8_t *scales,
+                              hipStream_t stream) {
+    if (n_elems < 0 || (n_elems > 0 && (!src || !packed || !scales)))
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (n_elems == 0) return GPTOSS_MOE_OK;
+    const int64_t nb = (n_elems + 31) / 32;
+    const int64_t need = (nb + 7) / 8;  // 8 blocks per 256-thread workgroup
+    const int grid = (int)(need < 16 * (int64_t)device_cus() ? need : 16 * (int64_t)device_cus());
+    hipLaunchKernelGGL(quantize_mxfp4_kernel, dim3(grid), dim3(256), 0, stream, src, n_elems, nb,
+                       packed, scales);
     return hip_status(hipGetLastError());
 }
 

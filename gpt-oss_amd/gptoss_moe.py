@@ -82,6 +82,7 @@ _SIGS = {
     "gptoss_moe_rmsnorm": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
     "gptoss_moe_dequant_mxfp4": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int64,
                                                 ctypes.c_int64, _VP, _VP]),
+    "gptoss_moe_quantize_mxfp4": (ctypes.c_int, [_VP, ctypes.c_int64, _VP, _VP, _VP]),
     "gptoss_moe_packed_size": (ctypes.c_size_t, [ctypes.POINTER(Shape)]),
     "gptoss_moe_pack_weights": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights),
                                                _VP, ctypes.c_size_t, _VP]),
@@ -298,3 +299,19 @@ def dequant_mxfp4(packed, scales, n_experts: int, n_rows: int, k_cols: int, stre
                                                  k_cols, _ptr(out), _stream(stream))
     _check("gptoss_moe_dequant_mxfp4", rc)
     return out
+
+
+def quantize_mxfp4(src, stream=None):
+    """fp32 device tensor -> (packed uint8 [ceil(n/32)*16], scales uint8 [ceil(n/32)])
+    with the reference loader's rule (gptoss_moe_quantize_mxfp4)."""
+    import torch
+    if src.dtype != torch.float32:
+        raise TypeError("quantize_mxfp4 takes float32")
+    s = src.contiguous().reshape(-1)
+    nb = (s.numel() + 31) // 32
+    packed = torch.empty(nb * 16, dtype=torch.uint8, device=s.device)
+    scales = torch.empty(nb, dtype=torch.uint8, device=s.device)
+    rc = load_library().gptoss_moe_quantize_mxfp4(_ptr(s), s.numel(), _ptr(packed), _ptr(scales),
+                                                  _stream(stream))
+    _check("gptoss_moe_quantize_mxfp4", rc)
+    return packed, scales

@@ -172,6 +172,19 @@ int gptoss_moe_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int n
                              hipStream_t stream);
 
 /*
+ * fp32 -> MXFP4 quantisation of a flattened array of n_elems values
+ * (quantize_pack_mxfp4_block32_kernel, memory/mxfp4.hpp:112-217, which the
+ * reference's loader runs on its fp32 weights): per 32-element block (the
+ * tail zero-filled) the e8m0 scale is ilogb(max |v|) - 2 + 127 (127 for an
+ * all-zero block, clamped to 0..255) and each element the nearest E2M1 code
+ * to v / 2^(scale-127), ties to the lower code index, NaN -> code 0.
+ * Writes ceil(n/32) * 16 bytes to packed (low nibble = even element) and
+ * ceil(n/32) bytes to scales: the layout gptoss_moe_weights expects.
+ */
+int gptoss_moe_quantize_mxfp4(const float *src, int64_t n_elems, uint8_t *packed, uint8_t *scales,
+                              hipStream_t stream);
+
+/*
  * Load-time weight packing (no counterpart in the reference, whose loader
  * converts weights once at start-up, getp_run.cpp:1041-1049): rearranges the
  * MXFP4 nibbles and e8m0 scales of w1 and w2 into MFMA fragment order for the

@@ -85,6 +85,55 @@ void orc_dequant_mxfp4_f32(const uint8_t *packed, const uint8_t *scales, int64_t
     for (int64_t i = 0; i < n; ++i) out[i] = orc_mxfp4_elem(packed, scales, i);
 }
 
+/*
+ * fp32 -> MXFP4 quantisation (quantize_pack_mxfp4_block32_kernel,
+ * mxfp4.hpp:112-217): per 32-element block of the flattened array (the tail
+ * block zero-filled), maxabs = max |v| over the block (NaN never wins: the
+ * reference's `a > maxabs` is false for NaN); exp = ilogb(maxabs) - 2 via
+ * frexpf (e - 1 - 2), 0 for an all-zero block; scale byte = clamp(exp + 127,
+ * 0, 255); each element the nearest E2M1 code to v / 2^exp by a brute-force
+ * scan with strict `<` (ties to the lower code index; NaN -> 0); two codes per
+ * byte, low nibble = even element.  packed: ceil(n/32) * 16 bytes,
+ * scales: ceil(n/32) bytes.
+ */
+void orc_quantize_mxfp4(const float *src, int64_t n, uint8_t *packed, uint8_t *scales) {
+    const int64_t nb = (n + 31) / 32;
+    for (int64_t b = 0; b < nb; ++b) {
+        float v[32];
+        for (int l = 0; l < 32; ++l) v[l] = (b * 32 + l < n) ? src[b * 32 + l] : 0.0f;
+        float maxabs = 0.0f;
+        for (int l = 0; l < 32; ++l) {
+            const float a = fabsf(v[l]);
+            if (a > maxabs) maxabs = a;
+        }
+        int exp_scale = 0;
+        if (maxabs > 0.0f) {
+            int e;
+            frexpf(maxabs, &e);
+            exp_scale = (e - 1) - 2;
+        }
+        int eb = exp_scale + 127;
+        scales[b] = (uint8_t)(eb < 0 ? 0 : (eb > 255 ? 255 : eb));
+        const float X = ldexpf(1.0f, exp_scale);
+        uint8_t nib[32];
+        for (int l = 0; l < 32; ++l) {
+            const float x = v[l] / X;
+            uint8_t best = 0;
+            float best_diff = fabsf(x - kE2M1[0]);
+            for (uint8_t i = 1; i < 16; ++i) {
+                const float dd = fabsf(x - kE2M1[i]);
+                if (dd < best_diff) {
+                    best_diff = dd;
+                    best = i;
+                }
+            }
+            nib[l] = best;
+        }
+        for (int q = 0; q < 16; ++q)
+            packed[b * 16 + q] = (uint8_t)((nib[2 * q + 1] << 4) | (nib[2 * q] & 0xF));
+    }
+}
+
 /* ------------------------------------------------------------- router -- */
 
 /*

@@ -25,6 +25,7 @@ _SIGS = {
     "orc_bf2f": (_F, [ctypes.c_uint16]),
     "orc_dequant_mxfp4": (None, [_P, _P, _I64, _P]),
     "orc_dequant_mxfp4_f32": (None, [_P, _P, _I64, _P]),
+    "orc_quantize_mxfp4": (None, [_P, _I64, _P, _P]),
     "orc_router_logits": (None, [_P, _P, _I, _I, _I, _P]),
     "orc_topk_softmax": (None, [_P, _P, _I, _I, _I, _P, _P]),
     "orc_route_index": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _P, _P]),
@@ -79,6 +80,16 @@ def dequant_f32(packed, scales, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().orc_dequant_mxfp4_f32(_p(packed), _p(scales), n, _p(out))
     return out
+
+
+def quantize_mxfp4(src):
+    """fp32 [n] -> (packed uint8 [ceil(n/32)*16], scales uint8 [ceil(n/32)])."""
+    s = _c(src, np.float32).reshape(-1)
+    nb = (s.size + 31) // 32
+    packed = np.zeros(nb * 16, np.uint8)
+    scales = np.zeros(nb, np.uint8)
+    lib().orc_quantize_mxfp4(_p(s), s.size, _p(packed), _p(scales))
+    return packed, scales
 
 
 def router_logits(x, wr) -> np.ndarray:

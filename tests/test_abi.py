@@ -87,3 +87,8 @@ def test_argument_errors_without_gpu():
                                 1 << 40, 8, None) == gm.ERR_UNSUPPORTED
     assert lib.gptoss_moe_rmsnorm(None, None, None, 1, 8, None) == gm.ERR_INVALID_ARG
     assert lib.gptoss_moe_dequant_mxfp4(None, None, 1, 1, 1, None, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_mxfp4(None, 32, None, None, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_mxfp4(None, -1, None, None, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_mxfp4(None, 0, None, None, None) == gm.OK
+    assert lib.gptoss_moe_pack_weights(None, None, None, 0, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_packed_size(None) == 0

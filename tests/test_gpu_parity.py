@@ -324,3 +324,55 @@ def test_zero_tokens_is_noop(gpu):
     layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
     x = torch.empty((0, d.cfg.hidden), dtype=torch.int16, device=gpu)
     layer.forward(x)
+
+
+# ------------------------------------------------------ MXFP4 quantiser --
+def _quant_case(seed):
+    rng = np.random.default_rng(seed)
+    return np.concatenate([
+        rng.standard_normal(32 * 4096).astype(np.float32) * np.float32(10.0) ** rng.integers(-3, 4, 32 * 4096),
+        (rng.integers(-24, 25, 32 * 512) * 0.25).astype(np.float32) * np.float32(2.0) ** rng.integers(-4, 5, 32 * 512),
+        np.zeros(64, np.float32),
+        np.ldexp(rng.standard_normal(64), -140).astype(np.float32),
+        np.array([np.nan, 1.0, -np.nan, 3.0] * 8, np.float32),
+        rng.standard_normal(77).astype(np.float32)]).astype(np.float32)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_quantize_mxfp4_bit_exact(gpu, seed):
+    """gptoss_moe_quantize_mxfp4 against the oracle byte for byte: magnitudes
+    1e-3..1e3, exact ties at code midpoints, zero and denormal blocks, NaN, a
+    ragged tail."""
+    import torch
+    import gptoss_moe
+    v = _quant_case(seed)
+    p, s = gptoss_moe.quantize_mxfp4(torch.from_numpy(v).to(gpu))
+    wp, ws = oracle.quantize_mxfp4(v)
+    assert np.array_equal(s.cpu().numpy(), ws)
+    assert np.array_equal(p.cpu().numpy(), wp)
+
+
+def test_quantize_mxfp4_round_trip_gpu(gpu):
+    """Quantise on the GPU, dequantise with the GEMMs' conversion: the result is
+    the oracle's dequantisation of the oracle's quantisation, bit for bit."""
+    import torch
+    import gptoss_moe
+    v = _quant_case(7)[:32 * 4096]
+    p, s = gptoss_moe.quantize_mxfp4(torch.from_numpy(v).to(gpu))
+    got = _host16(gptoss_moe.dequant_mxfp4(p, s, 1, 1, v.size))
+    wp, ws = oracle.quantize_mxfp4(v)
+    assert np.array_equal(got.reshape(-1), oracle.dequant(wp, ws, v.size).reshape(-1))
+
+
+def test_quantize_mxfp4_infinities(gpu):
+    """A block holding +-Inf: frexp of Inf gives exponent 0 in the C library,
+    so the scale is 2^-3; Inf itself becomes code 0 (every distance is
+    infinite) and the block's finite values saturate to +-6.  The device
+    library must agree byte for byte."""
+    import torch
+    import gptoss_moe
+    v = np.array([np.inf, -np.inf, 1.0, -1.0, 100.0] + [0.5] * 27 + [2.0] * 32, np.float32)
+    p, s = gptoss_moe.quantize_mxfp4(torch.from_numpy(v).to(gpu))
+    wp, ws = oracle.quantize_mxfp4(v)
+    assert np.array_equal(s.cpu().numpy(), ws)
+    assert np.array_equal(p.cpu().numpy(), wp)

@@ -254,3 +254,81 @@ def test_residual_add():
     got = bf16_to_f32(oracle.residual_add(a, b))
     big = float(bf16_to_f32(a)[3])  # bf16(1e4) = 9984; + 1 rounds back to it
     assert list(got) == [1.5, 2.0, 0.0, big]
+
+
+# ------------------------------------------------------ MXFP4 quantiser --
+E2M1 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+
+
+def _unpack(packed, n):
+    b = packed.astype(np.uint8)
+    nib = np.empty(b.size * 2, np.uint8)
+    nib[0::2] = b & 0xF
+    nib[1::2] = b >> 4
+    return nib[:n]
+
+
+def _quant_inputs(seed):
+    rng = np.random.default_rng(seed)
+    parts = [rng.standard_normal(32 * 64).astype(np.float32) * np.float32(10.0) ** rng.integers(-3, 4, 32 * 64),
+             (rng.integers(-24, 25, 32 * 16) * 0.25).astype(np.float32),      # ties at code midpoints
+             np.zeros(32, np.float32),                                          # all-zero block
+             np.ldexp(rng.standard_normal(32), -140).astype(np.float32),       # denormal block
+             rng.standard_normal(45).astype(np.float32)]                       # ragged tail
+    return np.concatenate(parts).astype(np.float32)
+
+
+def test_quantize_scale_rule():
+    """Scale byte = clip(floor(log2 max|v|) - 2 + 127, 0, 255), 127 for a zero
+    block (numpy frexp restatement, mxfp4.hpp:183-193)."""
+    v = _quant_inputs(1)
+    packed, scales = oracle.quantize_mxfp4(v)
+    nb = (v.size + 31) // 32
+    vv = np.zeros(nb * 32, np.float32)
+    vv[:v.size] = v
+    m = np.abs(vv.reshape(nb, 32)).max(axis=1)
+    _, e = np.frexp(m)
+    want = np.where(m > 0, np.clip(e - 3 + 127, 0, 255), 127).astype(np.uint8)
+    assert np.array_equal(scales, want)
+
+
+def test_quantize_nearest_code_first_index_ties():
+    """Each code is the first argmin of |v / 2^exp - E2M1[c]| (the reference's
+    strict-< scan keeps the lower index on ties), NaN -> 0.  exp is the
+    unclamped ilogb(max|v|) - 2: for a block of denormals it lies below -127,
+    the stored scale byte clamps to 0, and the codes still use 2^exp (the
+    reference's behaviour, mxfp4.hpp:188-201)."""
+    v = _quant_inputs(2)
+    v[5] = np.nan
+    packed, scales = oracle.quantize_mxfp4(v)
+    nb = scales.size
+    vv = np.zeros(nb * 32, np.float32)
+    vv[:v.size] = v
+    m = np.nanmax(np.abs(vv.reshape(nb, 32)), axis=1)
+    _, e = np.frexp(m)
+    ex = np.where(m > 0, e - 3, 0)
+    X = np.ldexp(np.float32(1), ex).astype(np.float32)
+    x = (vv.reshape(nb, 32) / X[:, None]).reshape(-1)
+    with np.errstate(invalid="ignore"):
+        d = np.abs(x[:, None] - E2M1[None, :])
+    d = np.where(np.isnan(d), np.inf, d)
+    want = d.argmin(axis=1).astype(np.uint8)
+    got = _unpack(packed, nb * 32)
+    assert np.array_equal(got, want)
+    assert got[5] == 0
+
+
+def test_quantize_round_trip_exact():
+    """Blocks built from E2M1 codes whose largest magnitude is 4 or 6 at a
+    scale come back unchanged (-0 comes back as +0)."""
+    rng = np.random.default_rng(3)
+    nb = 200
+    codes = rng.integers(0, 16, (nb, 32)).astype(np.uint8)
+    codes[:, 0] = rng.choice([6, 7, 14, 15], nb)  # |4| or |6| in every block
+    sc = rng.integers(100, 150, nb).astype(np.uint8)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8).reshape(-1)
+    vals = oracle.dequant_f32(packed, sc, nb * 32)
+    p2, s2 = oracle.quantize_mxfp4(vals)
+    assert np.array_equal(s2, sc)
+    want = np.where(codes.reshape(-1) == 8, 0, codes.reshape(-1))
+    assert np.array_equal(_unpack(p2, nb * 32), want)
