@@ -134,15 +134,20 @@ def main():
     for i in range(args.warmup):
         layers[i % copies].forward(x, out, fi, fw)
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # one event between consecutive steps (same stream): per-step times for
+    # the median and p90; the headline is the total over the K steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    ev0.record()
+    evs[0].record()
     for i in range(args.steps):
         layers[i % copies].forward(x, out, fi, fw)
-    ev1.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = evs[0].elapsed_time(evs[-1]) / args.steps
+    per_step = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+    ms_median = statistics.median(per_step)
+    ms_p90 = per_step[min(len(per_step) - 1, int(round(0.9 * (len(per_step) - 1))))]
 
     # per-kernel durations (HIP events between kernels on the launch stream)
     prof = {k: [] for k in gptoss_moe.MoeLayer.KERNELS}
@@ -173,6 +178,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_median": round(ms_median, 5),
+        "ms_per_step_p90": round(ms_p90, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
