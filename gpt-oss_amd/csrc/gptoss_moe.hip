@@ -1430,8 +1430,8 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
 //            l = (n = l & 15, g = l >> 4) holds, for q = 0..3, the 4 bytes of
 //            packed row 16 ct + n at row byte 64 kp + 16 q + 4 g (k = 128 kp +
 //            32 q + 8 g .. + 7); zero past K.
-//   scales:  [ct][kc < KC = ceil(K/256)][16 rows][8 B]: e8m0 of packed row
-//            16 ct + n for k groups 8 kc .. 8 kc + 7; zero past K/32.
+//   scales:  [ct][kq < KQ = ceil(K/512)][16 rows][16 B]: e8m0 of packed row
+//            16 ct + n for k groups 16 kq .. 16 kq + 15; zero past K/32.
 // Packed row pr is weight row pr for MLP2.  For MLP1 each 32-row group puts
 // its 16 gate rows (even) in column tile 0 and its 16 up rows in tile 1, so
 // one lane's two accumulators hold gate and up of the same output column.
@@ -1439,7 +1439,7 @@ struct PackLayout {
     size_t w1, s1, w2, s2, total;
 };
 inline size_t pk_w_expert(int N, int K) { return (size_t)N * ((K + 127) / 128) * 64; }
-inline size_t pk_s_expert(int N, int K) { return (size_t)N * ((K + 255) / 256) * 8; }
+inline size_t pk_s_expert(int N, int K) { return (size_t)N * ((K + 511) / 512) * 16; }
 PackLayout pack_layout(const gptoss_moe_shape &s) {
     const size_t E = (size_t)s.n_experts;
     const int H = s.hidden, D = s.intermediate;
@@ -1465,9 +1465,9 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
                                                   const uint8_t *__restrict__ ws, int N, int K,
                                                   int E, int mlp1, uint32_t *__restrict__ pw,
                                                   uint8_t *__restrict__ ps) {
-    const int KP = (K + 127) / 128, KC = (K + 255) / 256, CT = N / 16, KS = K / 32;
+    const int KP = (K + 127) / 128, KQ = (K + 511) / 512, CT = N / 16, KS = K / 32;
     const size_t nw = (size_t)E * CT * KP * 256;  // dwords
-    const size_t nsb = (size_t)E * CT * KC * 128;  // bytes
+    const size_t nsb = (size_t)E * CT * KQ * 256;  // bytes
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < nw + nsb;
          i += (size_t)gridDim.x * 256) {
         if (i < nw) {
@@ -1485,14 +1485,14 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
             pw[i] = v;
         } else {
             const size_t b = i - nw;
-            const int gi = (int)(b & 7), n = (int)((b >> 3) & 15);
-            size_t r = b >> 7;
-            const int kc = (int)(r % KC);
-            r /= KC;
+            const int gi = (int)(b & 15), n = (int)((b >> 4) & 15);
+            size_t r = b >> 8;
+            const int kq = (int)(r % KQ);
+            r /= KQ;
             const int ct = (int)(r % CT);
             const int e = (int)(r / CT);
             const int row = packed_src_row(16 * ct + n, mlp1 != 0);
-            const int grp = 8 * kc + gi;
+            const int grp = 16 * kq + gi;
             ps[b] = grp < KS ? ws[((size_t)e * N + row) * KS + grp] : (uint8_t)0;
         }
     }
@@ -1502,14 +1502,15 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
 //
 // Decode path on packed weights.  One workgroup of 8 waves per CU (2 per
 // SIMD), persistent over (tile of up to 64 rows of one expert, block of 256
-// weight rows) items (ItemMap order); K is swept in stages of 256 k.  Tiles
+// weight rows) items (ItemMap order); K is swept in stages of 512 k (the
+// per-stage synchronisation is paid once per 32 KB of weights).  Tiles
 // of 64 rows cover a whole decode expert, so each weight block streams once,
 // and a 256-row block halves the activation bytes per weight byte.
 // Every wave w streams its 2 column tiles (weight rows 32 w .. 32 w + 31 of
 // the block) straight from the packed weights into MFMA fragment registers
-// (2 x 16 B per tile per stage, one coalesced 1 KB access per instruction),
+// (4 x 16 B per tile per stage, one coalesced 1 KB access per instruction),
 // kDDepth stages ahead; weights never pass through LDS.  The stage's
-// activations (64 x 256 bf16), e8m0 scales (2 KB), biases and token slots go
+// activations (64 x 512 bf16), e8m0 scales (4 KB), biases and token slots go
 // to LDS by direct global -> LDS loads one stage ahead, shared out over the
 // waves.  A wave dequantises one k step ahead of its MFMAs
 // (v_mfma_f32_16x16x32_bf16), activations and scales read from LDS.
@@ -1523,16 +1524,20 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
 // The barrier is a plain s_barrier: a workgroup fence there would also drain
 // the loads of later stages.
 // MFMA lane l = (n = l & 15, g = l >> 4): in k step ks of stage j, slot
-// (g, e) stands for k = 256 j + 32 ks + 8 g + e in both operands.
+// (g, e) stands for k = 512 j + 32 ks + 8 g + e in both operands.
 constexpr int kDTileRows = 64;
 constexpr int kDBlockN = 256;
 constexpr int kDWaves = 8;
+constexpr int kDStageK = 512;          // k per stage
+constexpr int kDChunks = kDStageK / 128;  // 16-byte weight chunks per lane, tile and stage
+constexpr int kDUnits = kDStageK / 8;  // 16-byte activation units per row and stage
+constexpr int kDKSteps = kDStageK / 32;  // MFMA k steps per stage
 constexpr int kDDepth = 2;  // weight stages in flight (registers)
 constexpr int kDSlots = 2;  // LDS stages: the one computed and the one loading
-constexpr int kDALoads = kDTileRows * kUnits / 64 / kDWaves;  // 1 KB activation loads per wave
+constexpr int kDALoads = kDTileRows * kDUnits / 64 / kDWaves;  // 1 KB activation loads per wave
 struct DSlot {
-    uint4 a[kDTileRows * kUnits];   // tile row r, 16-byte unit u at r * 32 + (u ^ (r & 15))
-    uint2 sc[kDBlockN];             // e8m0 of the stage: column tile c, row n at 16 c + n
+    uint4 a[kDTileRows * kDUnits];  // tile row r, 16-byte unit u at r * 64 + (u ^ (r & 15))
+    uint4 sc[kDBlockN];             // e8m0 of the stage: column tile c, row n at 16 c + n
     uint16_t bias[kDBlockN];        // bias of block rows 0..255 (weight-row order)
     int32_t slot[kDTileRows];       // token-order slot of tile row r (MLP2)
 };
@@ -1540,7 +1545,7 @@ struct DSlot {
 struct DArgs {
     GemmArgs g;
     const uint4 *pw;      // packed nibbles of this matrix
-    const uint2 *ps;      // packed scales
+    const uint4 *ps;      // packed scales (16 per row and stage)
 };
 
 // s_waitcnt vmcnt(N), other counters left alone (gfx9 encoding).
@@ -1578,26 +1583,35 @@ __device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
 __device__ __forceinline__ void lds_wait(u32x4 &v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
 __device__ __forceinline__ void lds_wait(uint32_t &v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
 
-__device__ __forceinline__ uint2 lds_read_b64(uint32_t addr) {
-    uint2 v;
-    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+// Direct global -> LDS loads of 16 / 4 bytes per lane (lane l writes lds +
+// l * size; lds must be wave-uniform).
+__device__ __forceinline__ void lds_dma16(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+}
+// The value unchanged, but opaque to the compiler: expressions built on it
+// are computed where they are used, not hoisted out of the K loop into
+// registers that stay live across it.
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+    asm volatile("" : "+v"(v));
     return v;
 }
-__device__ __forceinline__ void lds_wait(uint2 &v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
 
 template <int MT>
-__device__ __forceinline__ void direct_stage(const DSlot &sl, const uint4 (&w)[2][2],
+__device__ __forceinline__ void direct_stage(const DSlot &sl, const uint4 (&w)[2][kDChunks],
                                              f32x4 (&acc)[4][2]) {
     const int lane = threadIdx.x & 63, n_l = lane & 15, g = lane >> 4;
     const int wave = threadIdx.x >> 6;
-    const uint32_t abase = lds_addr(sl.a);
-    uint2 sc[2];
+    const uint32_t abase = opaque_vgpr(lds_addr(sl.a));
+    u32x4 sc[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) sc[t] = lds_read_b64(lds_addr(&sl.sc[16 * (2 * wave + t) + n_l]));
+    for (int t = 0; t < 2; ++t) sc[t] = lds_read_b128_at<0>(lds_addr(&sl.sc[16 * (2 * wave + t) + n_l]));
 #pragma unroll
     for (int t = 0; t < 2; ++t) lds_wait(sc[t]);
     auto deq = [&](int ks, int t) {
-        const uint32_t sw = ks < 4 ? sc[t].x : sc[t].y;
+        const uint32_t sw = sc[t][ks >> 2];
         const uint32_t e = (sw >> (8 * (ks & 3))) & 0xffu;
         // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
         const uint32_t zm = e == 0 ? 0x88888888u : 0xffffffffu;
@@ -1606,21 +1620,22 @@ __device__ __forceinline__ void direct_stage(const DSlot &sl, const uint4 (&w)[2
         return dequant8(dw & zm, e8m0_to_f32(e));
     };
     // activation fragments of k step ks: row 16 m + n_l, unit (4 ks + g) ^ n_l
-    // = lane part 16 (n_l * 32 + (g ^ (n_l & 3))) + 64 (ks ^ (n_l >> 2)), and
-    // row group m at the immediate offset m * 32 rows * 512 B
-    const uint32_t alane = abase + 16u * (uint32_t)(n_l * kUnits + (g ^ (n_l & 3)));
+    // = lane part 16 (n_l * 64 + (g ^ (n_l & 3))) + 64 (ks ^ (n_l >> 2)), and
+    // row group m at the immediate offset m * 16 rows * 1 KB
+    const uint32_t alane = abase + 16u * (uint32_t)(n_l * kDUnits + (g ^ (n_l & 3)));
     auto areads = [&](int ks, u32x4 (&v)[MT]) {
         const uint32_t ad = alane + 64u * (uint32_t)(ks ^ (n_l >> 2));
+        constexpr uint32_t G = 16 * kDUnits * 16;  // bytes per 16-row group
         v[0] = lds_read_b128_at<0>(ad);
-        if constexpr (MT > 1) v[1] = lds_read_b128_at<16 * kUnits * 16>(ad);
-        if constexpr (MT > 2) v[2] = lds_read_b128_at<2 * 16 * kUnits * 16>(ad);
-        if constexpr (MT > 3) v[3] = lds_read_b128_at<3 * 16 * kUnits * 16>(ad);
+        if constexpr (MT > 1) v[1] = lds_read_b128_at<G>(ad);
+        if constexpr (MT > 2) v[2] = lds_read_b128_at<2 * G>(ad);
+        if constexpr (MT > 3) v[3] = lds_read_b128_at<3 * G>(ad);
     };
     u32x4 an[MT];
     areads(0, an);
     bf16x8 bn0 = deq(0, 0), bn1 = deq(0, 1);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < kDKSteps; ++ks) {
         const bf16x8 b0 = bn0, b1 = bn1;
         bf16x8 af[MT];
 #pragma unroll
@@ -1628,7 +1643,7 @@ __device__ __forceinline__ void direct_stage(const DSlot &sl, const uint4 (&w)[2
             lds_wait(an[m]);
             af[m] = __builtin_bit_cast(bf16x8, an[m]);
         }
-        if (ks < 7) {
+        if (ks < kDKSteps - 1) {
             areads(ks + 1, an);
             bn0 = deq(ks + 1, 0);
             bn1 = deq(ks + 1, 1);
@@ -1674,12 +1689,14 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs &a, const DSlot &
         // bias of columns wcol0 + n_l and + 16 (low / high half of an aligned pair)
         uint32_t b0 = lds_read_b32(lds_addr(&sl.bias[(32 * w + n_l) & ~1]));
         uint32_t b1 = lds_read_b32(lds_addr(&sl.bias[(32 * w + 16 + n_l) & ~1]));
+        // slot addresses from one opaque base: computed here, not hoisted
+        const uint32_t sbase = opaque_vgpr(lds_addr(&sl.slot[4 * g]));
         uint32_t sv[MT][4];
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                sv[m][v] = lds_read_b32(lds_addr(&sl.slot[16 * m + 4 * g + v]));
+                sv[m][v] = lds_read_b32(sbase + 4u * (uint32_t)(16 * m + v));
         lds_wait(b0);
         lds_wait(b1);
         float bb[2];
@@ -1707,7 +1724,7 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     ItemMap im;
     int n_items;
     im.init(a.hdr, (a.N + kDBlockN - 1) / kDBlockN, n_items);
-    const int NST = (a.K + kStageK - 1) / kStageK;
+    const int NST = (a.K + kDStageK - 1) / kDStageK;
     if (n_items == 0) return;
     const int total = n_items * NST;
     const int total_p = (total + kDDepth - 1) / kDDepth * kDDepth;
@@ -1715,8 +1732,8 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int N = a.N, K = a.K;
-    const int CT = N / 16, KP = (K + 127) / 128, KC = (K + 255) / 256;
-    uint4 wr[kDDepth][2][2];
+    const int CT = N / 16, KP = (K + 127) / 128, KQ = (K + 511) / 512;
+    uint4 wr[kDDepth][2][kDChunks];
     StepCursor wcur, lcur, ccur;
 #ifdef GPTOSS_TRACE
     int lds_count = 0;  // this wave's LDS loads of the last issued stage
@@ -1726,7 +1743,7 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     lcur.init(a, im, n_items);
     ccur.init(a, im, n_items);
 
-    // Weights of stage st (2 column tiles x 2 x 16 B per lane) into ring slot r.
+    // Weights of stage st (2 column tiles x kDChunks x 16 B per lane) into ring slot r.
     auto issue_w = [&](int st, int r) {
         st = min(st, total - 1);
         Tile tl;
@@ -1737,8 +1754,8 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
             const int ct = min(nb * (kDBlockN / 16) + 2 * w + t, CT - 1);  // past N: unused data
             const size_t tile = (size_t)tl.expert * CT + ct;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                wr[r][t][h] = d.pw[(tile * KP + min(2 * j + h, KP - 1)) * 64 + lane];
+            for (int h = 0; h < kDChunks; ++h)
+                wr[r][t][h] = d.pw[(tile * KP + min(kDChunks * j + h, KP - 1)) * 64 + lane];
         }
     };
     // Direct global -> LDS loads of stage st into slot st % kDSlots.  Only
@@ -1751,45 +1768,40 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
         int nb, j;
         lcur.at(a, im, NST, st, tl, nb, j);
 #ifdef GPTOSS_TRACE
-        lds_count = min(max(((tl.rows + 15) & ~15) / 2 - kDALoads * w, 0), kDALoads) + (w < 5 ? 1 : 0);
+        lds_count = min(max(((tl.rows + 15) & ~15) - kDALoads * w, 0), kDALoads) + (w < 7 ? 1 : 0);
 #endif
-        // activations: load i of wave w fills LDS units 64 q .. 64 q + 63,
-        // q = kDALoads w + i (tile rows 2 q, 2 q + 1); lane l fetches the unit
-        // its LDS position stands for under the row swizzle.  Rows past the
-        // tile repeat its last row, k past K the last unit (against zero
-        // weights).
+        // activations: load i of wave w fills LDS row q = kDALoads w + i
+        // (64 units of 16 B); lane l fetches the unit its LDS position stands
+        // for under the row swizzle.  Rows past the tile repeat its last row,
+        // k past K the last unit (against zero weights).
         const char *base = reinterpret_cast<const char *>(a.A + (size_t)tl.row0 * K);
         const int rmax = tl.rows - 1;
         const int rpad = (tl.rows + 15) & ~15;  // rows the MFMAs read
+        const int ln = (int)opaque_vgpr((uint32_t)lane);
 #pragma unroll
         for (int i = 0; i < kDALoads; ++i) {
             const int q = kDALoads * w + i;
-            if (2 * q < rpad) {
-                const int x = 64 * q + lane;
-                const int rr = x >> 5, u = (x & 31) ^ (rr & 15);
-                const uint32_t off = (uint32_t)min(rr, rmax) * (2u * K) +
-                                     2u * (uint32_t)min(j * kStageK + 8 * u, K - 8);
-                __builtin_amdgcn_global_load_lds(base + off, &sl.a[64 * q], 16, 0, 0);
+            if (q < rpad) {
+                const int u = ln ^ (q & 15);
+                const uint32_t off = (uint32_t)min(q, rmax) * (2u * K) +
+                                     2u * (uint32_t)min(j * kDStageK + 8 * u, K - 8);
+                lds_dma16(base + off, &sl.a[64 * q]);
             }
         }
-        // LDS destinations as element addresses: an array argument is not
-        // decayed to a pointer by this builtin
-        if (w < 2) {
-            // scales: 16 column tiles x 128 B; wave w loads tiles 8 w .. 8 w + 7
-            // (lane l: tile 8 w + (l >> 3), 16-byte part l & 7)
-            const int ct = min(nb * (kDBlockN / 16) + 8 * w + (lane >> 3), CT - 1);
-            const char *src = reinterpret_cast<const char *>(d.ps) +
-                              ((((size_t)tl.expert * CT + ct) * KC + j) * 128 + 16 * (lane & 7));
-            __builtin_amdgcn_global_load_lds(src, &sl.sc[128 * w], 16, 0, 0);
-        } else if (w < 4) {
-            // biases of block rows 128 (w - 2) .. + 127, 2 per lane
-            const int h = w - 2;
-            __builtin_amdgcn_global_load_lds(
-                a.bias + (size_t)tl.expert * N + min(nb * kDBlockN + 128 * h + 2 * lane, N - 2),
-                &sl.bias[128 * h], 4, 0, 0);
-        } else if (w == 4) {
-            __builtin_amdgcn_global_load_lds(a.row_slot + tl.row0 + min(lane, rmax), &sl.slot[0],
-                                             4, 0, 0);
+        // LDS destinations as element addresses (an array argument is not
+        // decayed to a pointer by the builtin)
+        if (w < 4) {
+            // scales: 16 column tiles x 16 rows x 16 B; wave w loads tiles
+            // 4 w .. 4 w + 3 (lane l: tile 4 w + (l >> 4), row l & 15)
+            const int ct = min(nb * (kDBlockN / 16) + 4 * w + (lane >> 4), CT - 1);
+            lds_dma16(&d.ps[(((size_t)tl.expert * CT + ct) * KQ + j) * 16 + (lane & 15)], &sl.sc[64 * w]);
+        } else if (w < 6) {
+            // biases of block rows 128 (w - 4) .. + 127, 2 per lane
+            const int h = w - 4;
+            lds_dma4(a.bias + (size_t)tl.expert * N + min(nb * kDBlockN + 128 * h + 2 * lane, N - 2),
+                     &sl.bias[128 * h]);
+        } else if (w == 6) {
+            lds_dma4(a.row_slot + tl.row0 + min(lane, rmax), &sl.slot[0]);
         }
     };
 
@@ -1820,20 +1832,24 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
             const int s = s0 + r;
             __builtin_amdgcn_sched_barrier(0);
             // behind stage s's LDS loads only weight loads were issued: the
-            // last kDDepth - 1 stages' (4 each) may stay in flight
+            // last kDDepth - 1 stages' (2 kDChunks each) may stay in flight
 #ifdef GPTOSS_TRACE
             // weights of stage s only (issued before stage s's LDS loads)
             switch (lds_count) {
-            case 0: wait_vmcnt<4>(); break;
-            case 1: wait_vmcnt<5>(); break;
-            case 2: wait_vmcnt<6>(); break;
-            case 3: wait_vmcnt<7>(); break;
-            case 4: wait_vmcnt<8>(); break;
-            default: wait_vmcnt<9>(); break;
+            case 0: wait_vmcnt<2 * kDChunks>(); break;
+            case 1: wait_vmcnt<2 * kDChunks + 1>(); break;
+            case 2: wait_vmcnt<2 * kDChunks + 2>(); break;
+            case 3: wait_vmcnt<2 * kDChunks + 3>(); break;
+            case 4: wait_vmcnt<2 * kDChunks + 4>(); break;
+            case 5: wait_vmcnt<2 * kDChunks + 5>(); break;
+            case 6: wait_vmcnt<2 * kDChunks + 6>(); break;
+            case 7: wait_vmcnt<2 * kDChunks + 7>(); break;
+            case 8: wait_vmcnt<2 * kDChunks + 8>(); break;
+            default: wait_vmcnt<2 * kDChunks + 9>(); break;
             }
             DTR(tw)
 #endif
-            wait_vmcnt<4 * (kDDepth - 1)>();
+            wait_vmcnt<2 * kDChunks * (kDDepth - 1)>();
             DTR(twl)
             __builtin_amdgcn_s_barrier();  // everyone's loads of stage s landed; slot (s+1) % 2 is free
             __builtin_amdgcn_sched_barrier(0);
@@ -1847,13 +1863,13 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
                 Tile tl;
                 int nb, j;
                 ccur.at(a, im, NST, s, tl, nb, j);
-                uint4(&wv)[2][2] = wr[r];
+                uint4(&wv)[2][kDChunks] = wr[r];
                 // k groups of a stage past K: kp >= KP is a clamped reload, zero it
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const uint32_t km = -(uint32_t)(2 * j + h < KP);
+                    for (int h = 0; h < kDChunks; ++h) {
+                        const uint32_t km = -(uint32_t)(kDChunks * j + h < KP);
                         wv[t][h] = make_uint4(wv[t][h].x & km, wv[t][h].y & km, wv[t][h].z & km,
                                               wv[t][h].w & km);
                     }
@@ -2273,7 +2289,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     else if (direct)
         hipLaunchKernelGGL(direct_gemm_kernel<true>, dim3(cap), dim3(kDWaves * 64), 0, st,
                            DArgs{a1, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
-                                 reinterpret_cast<const uint2 *>(w->packed + PL.s1)});
+                                 reinterpret_cast<const uint4 *>(w->packed + PL.s1)});
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a1);
     if (mk) mk->mark(st);
@@ -2293,7 +2309,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     else if (direct)
         hipLaunchKernelGGL(direct_gemm_kernel<false>, dim3(cap), dim3(kDWaves * 64), 0, st,
                            DArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
-                                 reinterpret_cast<const uint2 *>(w->packed + PL.s2)});
+                                 reinterpret_cast<const uint4 *>(w->packed + PL.s2)});
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a2);
     if (mk) mk->mark(st);

@@ -166,99 +166,96 @@ def test_large_m_loads_in_bounds(N, K):
 
 
 # ------------------------------------------------- direct GEMM (packed) --
-DBN, DTR, DWAVES = 256, 64, 8  # weight rows per item, activation rows per tile, waves
+DBN, DTR, DWAVES, DSK = 256, 64, 8, 512  # weight rows per item, tile rows, waves, k per stage
+DCH = DSK // 128                          # 16-byte weight chunks per lane, tile and stage
 
 
 def direct_weight_loads(N, K, E):
-    """direct_gemm_kernel issue_w(): per lane 2 tiles x 2 16-byte nibble loads
-    (uint4 index) per stage, for every expert, weight block, wave and stage;
-    and issue_lds()'s scale loads (byte offsets, waves 0 and 1)."""
-    CT, KP, KC = N // 16, -(-K // 128), -(-K // 256)
-    nst = -(-K // STAGE_K)
+    """direct_gemm_kernel issue_w(): per lane 2 tiles x DCH 16-byte nibble
+    loads (uint4 index) per stage, for every expert, weight block, wave and
+    stage; and issue_lds()'s scale loads (uint4 index, waves 0..3)."""
+    CT, KP, KQ = N // 16, -(-K // 128), -(-K // 512)
+    nst = -(-K // DSK)
     lane = np.arange(64)
-    w_idx, s_off = [], []
+    w_idx, s_idx = [], []
     for e in (0, E - 1):
         for nb in range(-(-N // DBN)):
             for j in range(nst):
                 for w in range(DWAVES):
                     for t in range(2):
                         tile = e * CT + min(nb * (DBN // 16) + 2 * w + t, CT - 1)
-                        for h in range(2):
-                            w_idx.append((tile * KP + min(2 * j + h, KP - 1)) * 64 + lane)
-                for w in range(2):
-                    ct = np.minimum(nb * (DBN // 16) + 8 * w + (lane >> 3), CT - 1)
-                    s_off.append(((e * CT + ct) * KC + j) * 128 + 16 * (lane & 7))
-    return np.concatenate(w_idx), np.concatenate(s_off)
+                        for h in range(DCH):
+                            w_idx.append((tile * KP + min(DCH * j + h, KP - 1)) * 64 + lane)
+                for w in range(4):
+                    ct = np.minimum(nb * (DBN // 16) + 4 * w + (lane >> 4), CT - 1)
+                    s_idx.append(((e * CT + ct) * KQ + j) * 16 + (lane & 15))
+    return np.concatenate(w_idx), np.concatenate(s_idx)
 
 
 @pytest.mark.parametrize("N,K", [(256, 128), (128, 128), (192, 448), (896, 192), (5760, 2880),
                                  (2880, 2880), (128, 64), (6144, 3072), (64, 3072)])
 def test_direct_weight_loads_in_bounds(N, K):
     E = 3
-    w_idx, s_off = direct_weight_loads(N, K, E)
-    # packed sizes per expert: N * ceil(K/128) * 64 nibble bytes, N * ceil(K/256) * 8 scale bytes
+    w_idx, s_idx = direct_weight_loads(N, K, E)
+    # packed sizes per expert: N * ceil(K/128) * 64 nibble bytes, N * ceil(K/512) * 16 scale bytes
     assert w_idx.min() >= 0 and (w_idx.max() + 1) * 16 <= E * N * -(-K // 128) * 64
-    assert s_off.min() >= 0 and s_off.max() + 16 <= E * N * -(-K // 256) * 8
-    # the LDS scale block holds column tile c, row n at uint2 16 c + n: lane l of
-    # wave w writes bytes 16 l .. of the w-th 1 KB half, i.e. tile 8 w + (l >> 3)
+    assert s_idx.min() >= 0 and (s_idx.max() + 1) * 16 <= E * N * -(-K // 512) * 16
 
 
 def direct_activation_loads(K, rows, j):
-    """issue_lds(): for every wave and its 4 loads, the LDS unit group it fills
-    and the byte offsets (from the tile's first row) its lanes read; row pairs
-    at or past the 16-row padding of the tile are not loaded."""
+    """issue_lds(): for every wave and its loads, the LDS row it fills (64
+    units of 16 B, lane l at unit 64 q + l) and the byte offsets (from the
+    tile's first row) its lanes read; rows at or past the tile's 16-row
+    padding are not loaded."""
     lane = np.arange(64)
     rpad = (rows + 15) & ~15
     units, offs = [], []
     for w in range(DWAVES):
-        for i in range(DTR * 32 // 64 // DWAVES):
-            q = 4 * w + i
-            if 2 * q >= rpad:
+        for i in range(DTR * (DSK // 8) // 64 // DWAVES):
+            q = (DTR * (DSK // 8) // 64 // DWAVES) * w + i
+            if q >= rpad:
                 continue
-            x = 64 * q + lane
-            r = x >> 5
-            u = (x & 31) ^ (r & 15)
-            units.append(x)
-            offs.append(np.minimum(r, rows - 1) * 2 * K + 2 * np.minimum(j * STAGE_K + 8 * u, K - 8))
+            u = lane ^ (q & 15)
+            units.append(64 * q + lane)
+            offs.append(np.minimum(q, rows - 1) * 2 * K + 2 * np.minimum(j * DSK + 8 * u, K - 8))
     return np.concatenate(units), np.concatenate(offs), rpad
 
 
 @pytest.mark.parametrize("K", [64, 128, 448, 2880])
 @pytest.mark.parametrize("rows", [1, 16, 17, 33, 63, 64])
 def test_direct_activation_loads(K, rows):
-    for j in range(-(-K // STAGE_K)):
+    for j in range(-(-K // DSK)):
         units, offs, rpad = direct_activation_loads(K, rows, j)
         # every LDS unit of the rows the MFMAs read is written exactly once
-        assert np.array_equal(np.sort(units), np.arange(rpad * 32))
+        assert np.array_equal(np.sort(units), np.arange(rpad * 64))
         # reads stay inside the tile's rows
         assert offs.min() >= 0 and (offs + 16).max() <= rows * 2 * K
         assert (offs % 16 == 0).all()
-        # the consumer's fragment (row r, unit U) sits at LDS unit r*32 + (U ^ (r & 15)):
+        # the consumer's fragment (row r, unit U) sits at LDS unit r*64 + (U ^ (r & 15)):
         # the loader put source row r (clamped), k unit U there
-        got = np.full(DTR * 32, -1, np.int64)
+        got = np.full(DTR * 64, -1, np.int64)
         got[units] = offs
-        r = np.repeat(np.arange(rpad), 32)
-        U = np.tile(np.arange(32), rpad)
-        pos = r * 32 + (U ^ (r & 15))
-        want = np.minimum(r, rows - 1) * 2 * K + 2 * np.minimum(j * STAGE_K + 8 * U, K - 8)
+        r = np.repeat(np.arange(rpad), 64)
+        U = np.tile(np.arange(64), rpad)
+        pos = r * 64 + (U ^ (r & 15))
+        want = np.minimum(r, rows - 1) * 2 * K + 2 * np.minimum(j * DSK + 8 * U, K - 8)
         assert np.array_equal(got[pos], want)
-        # the consumer's address form: lane part + 64 (ks ^ (n >> 2)) + m * 8192 bytes
+        # the consumer's address form: lane part + 64 (ks ^ (n >> 2)) + m * 16 KB
         n = r & 15
         ks, g = U >> 2, U & 3
         m = r >> 4
-        assert np.array_equal(16 * pos, 16 * (n * 32 + (g ^ (n & 3))) + 64 * (ks ^ (n >> 2)) + m * 8192)
+        assert np.array_equal(16 * pos, 16 * (n * 64 + (g ^ (n & 3))) + 64 * (ks ^ (n >> 2)) + m * 16384)
 
 
 @pytest.mark.parametrize("N", [128, 192, 384, 5760, 2880])
 def test_direct_aux_loads(N):
-    """Bias pairs (waves 2, 3: 4 bytes at element min(256 nb + 128 h + 2 l, N - 2))
+    """Bias pairs (waves 4, 5: 4 bytes at element min(256 nb + 128 h + 2 l, N - 2))
     stay inside the expert's N biases; slot loads stay inside the tile."""
     lane = np.arange(64)
     for nb in range(-(-N // DBN)):
         for h in range(2):
             b = np.minimum(nb * DBN + 128 * h + 2 * lane, N - 2)
             assert b.min() >= 0 and b.max() + 2 <= N
-            # a block row's bias sits at LDS element (row - 256 nb) when the row exists
             row = nb * DBN + 128 * h + 2 * lane
             ok = row < N
             assert np.array_equal(b[ok], row[ok])
