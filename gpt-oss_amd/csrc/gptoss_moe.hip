@@ -20,6 +20,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "../../include/gptoss_moe.h"
 
 namespace {
@@ -72,15 +74,16 @@ __device__ __forceinline__ uint32_t zero_scale_fix(uint32_t q, uint32_t e) {
 
 // ------------------------------------------------------- workspace map --
 struct WsLayout {
-    size_t hdr, hist, blkbase, counts, offsets, tiles, logits, topk_i, topk_w, slot_e, local_ids,
+    size_t hdr, hist, counts, offsets, tiles, logits, topk_i, topk_w, slot_e, local_ids,
         row_token, row_w, row_slot, xg, act, slots, total;
     int max_tiles;
 };
 
-// hdr ints: NTILES = tile count, STATUS = dropped slots of the last call.
+// hdr ints: NTILES = tile count, STATUS = dropped slots of the last call,
+// DONE = index workgroups past their histogram reads (0 between calls).
 // XSTART / XCOUNT: the tile list is grouped by XCD; tiles of XCD x are
 // tiles[XSTART + x] .. + [XCOUNT + x].
-enum { HDR_NTILES = 1, HDR_STATUS = 4, HDR_XSTART = 8, HDR_XCOUNT = 16, HDR_INTS = 256 };
+enum { HDR_NTILES = 1, HDR_DONE = 2, HDR_STATUS = 4, HDR_XSTART = 8, HDR_XCOUNT = 16, HDR_INTS = 256 };
 // Diagnostic builds (-DGPTOSS_TRACE) accumulate per-role cycle counts into the
 // header bytes 512..1023 (64 x u64); the product build compiles this away.
 #ifdef GPTOSS_TRACE
@@ -107,7 +110,6 @@ WsLayout ws_layout(const gptoss_moe_shape &s, int max_tokens) {
     };
     L.hdr = take(HDR_INTS * 4);
     L.hist = take((size_t)kMaxBlocks * kHistCols * 4);
-    L.blkbase = take((size_t)kMaxBlocks * E * 4);
     L.counts = take(E * 4);
     L.offsets = take((E + 1) * 4);
     L.tiles = take((size_t)L.max_tiles * 16);
@@ -131,6 +133,40 @@ struct Tile {
 };
 
 // ------------------------------------------------------------- routing --
+// Workgroup barrier that orders LDS only: global stores still in flight are
+// not waited for (__syncthreads would drain them).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Cross-lane moves without the LDS crossbar (DPP and gfx950 permlane swaps).
+// xor16<S>: lane l gets lane l ^ S (S = 1, 2, 4, 8; inside 16-lane rows).
+template <int S>
+__device__ __forceinline__ int xor16(int v) {
+    static_assert(S == 1 || S == 2 || S == 4 || S == 8, "xor16 stride");
+    if constexpr (S == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);   // quad_perm 1,0,3,2
+    if constexpr (S == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);   // quad_perm 2,3,0,1
+    if constexpr (S == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // row_ror:8
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, false);    // row_shl:4 (lane l + 4)
+    const int down = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4 (lane l - 4)
+    return (threadIdx.x & 4) ? down : up;
+}
+template <int S>
+__device__ __forceinline__ float xor16(float v) {
+    return __int_as_float(xor16<S>(__float_as_int(v)));
+}
+// down64<S>: lanes l < S get lane l + S (S = 1 .. 32); other lanes undefined.
+template <int S>
+__device__ __forceinline__ int down64(int v) {
+    if constexpr (S == 32) return (int)__builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false)[1];
+    else if constexpr (S == 16) return (int)__builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false)[1];
+    else return __builtin_amdgcn_update_dpp(0, v, 0x100 + S, 0xf, 0xf, false);  // row_shl:S
+}
+template <int S>
+__device__ __forceinline__ float down64(float v) {
+    return __int_as_float(down64<S>(__float_as_int(v)));
+}
+
 // better_pick of moe.hpp:333-342 with the multiplies and adds kept unfused
 // so the comparison rounds exactly as written.
 __device__ __forceinline__ bool better_pick(float av, int ai, float bv, int bi) {
@@ -141,15 +177,16 @@ __device__ __forceinline__ bool better_pick(float av, int ai, float bv, int bi) 
     return false;
 }
 
-// Routing is three kernels with no synchronisation between workgroups inside
-// any of them (on a multi-XCD part a device-scope fence writes back and
-// invalidates the XCD's L2, which costs more than a kernel boundary):
-//   route_kernel         router logits + top-k/softmax for TB tokens per
-//                        workgroup, and a per-block expert histogram;
-//   plan_kernel          one workgroup: counts, offsets, per-block row bases,
-//                        the tile list; clears the histogram for the next call;
-//   index_gather_kernel  compact row map (ascending token order per expert)
-//                        and the gather of x rows into compact order.
+// Routing is two kernels with no fence between workgroups inside either (on
+// a multi-XCD part a device-scope fence writes back and invalidates the XCD's
+// L2, which costs more than a kernel boundary):
+//   route_kernel   router logits + top-k/softmax for TB tokens per
+//                  workgroup, and a per-block expert histogram (device-scope
+//                  atomics);
+//   index_kernel   per workgroup the histogram scan (counts, offsets, the
+//                  tile list, its block's row bases), the compact row map
+//                  (ascending token order per expert) and, for the LDS-staged
+//                  GEMMs, the gather of x rows into compact order.
 // Histogram blocks are runs of block_tokens tokens (a multiple of 64, at most
 // kMaxBlocks blocks per call); column E counts dropped slots.
 
@@ -277,8 +314,10 @@ __global__ __launch_bounds__(256) void route_kernel(
 #pragma unroll
             for (int j = 0; j < EE; ++j) {
                 float s = acc[tt][j];
-#pragma unroll
-                for (int st = 8; st >= 1; st >>= 1) s = __fadd_rn(s, __shfl_xor(s, st, 16));
+                s = __fadd_rn(s, xor16<8>(s));
+                s = __fadd_rn(s, xor16<4>(s));
+                s = __fadd_rn(s, xor16<2>(s));
+                s = __fadd_rn(s, xor16<1>(s));
                 const int e = grp * EE + j;
                 if (l16 == 0 && e < E && tt < nt) {
                     const uint16_t b = f2bf(s);
@@ -286,7 +325,7 @@ __global__ __launch_bounds__(256) void route_kernel(
                     sc[tt][e] = bf2f(b);
                 }
             }
-        __syncthreads();
+        lds_barrier();  // sc complete; the logits stores need not have landed
 
         // ---- top-k + softmax, one wave per token
         const int R = nthreads_ref / 64;  // 1, 2 or 4 slots per lane
@@ -333,17 +372,23 @@ __global__ __launch_bounds__(256) void route_kernel(
                 float bv = cv[0];
                 int bi = ci[0];
                 // tree strides 32..1: lane l < st takes lane l+st's pick if better
-#pragma unroll
-                for (int st = 32; st >= 1; st >>= 1) {
-                    const float ov = __shfl_down(bv, st, 64);
-                    const int oi = __shfl_down(bi, st, 64);
+                auto step = [&](auto st_c) {
+                    constexpr int st = decltype(st_c)::value;
+                    const float ov = down64<st>(bv);
+                    const int oi = down64<st>(bi);
                     if (lane < st && better_pick(ov, oi, bv, bi)) {
                         bv = ov;
                         bi = oi;
                     }
-                }
-                bv = __shfl(bv, 0, 64);
-                bi = __shfl(bi, 0, 64);
+                };
+                step(std::integral_constant<int, 32>());
+                step(std::integral_constant<int, 16>());
+                step(std::integral_constant<int, 8>());
+                step(std::integral_constant<int, 4>());
+                step(std::integral_constant<int, 2>());
+                step(std::integral_constant<int, 1>());
+                bv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bv)));
+                bi = __builtin_amdgcn_readfirstlane(bi);
                 sel_i[s] = bi;
                 sel_v[s] = bv;
                 if (bi < E && (bi & 63) == lane) visited |= 1u << (bi >> 6);
@@ -388,19 +433,22 @@ __global__ __launch_bounds__(256) void route_kernel(
             }
         }
     }
-    __syncthreads();
+    lds_barrier();  // shist complete
     int32_t *hrow = hist + (size_t)(t0 / block_tokens) * kHistCols;
     for (int c = tid; c <= E; c += 256)
         if (shist[c]) atomicAdd(&hrow[c], shist[c]);
 }
 
-// Wave-inclusive scan of v over 64 lanes.
+// Wave-inclusive scan of v over 64 lanes (DPP: row shifts, then the row
+// broadcasts of lanes 15 and 31).
 __device__ __forceinline__ int wave_scan(int v, int lane) {
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const int o = __shfl_up(v, s, 64);
-        if (lane >= s) v += o;
-    }
+    (void)lane;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
     return v;
 }
 
@@ -418,7 +466,7 @@ __device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x)
 // XCD x occupy tiles[xstart(x) .. xstart(x) + xcount(x)), 2-tile units first.
 __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ counts,
                             int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr,
-                            int E, int tr, int lane) {
+                            int E, int tr, int lane, bool write) {
     // lane l owns experts 4l .. 4l+3
     int c[4], nt[4], n2[4], n1[4];
     int csum = 0, s2 = 0, s1 = 0;
@@ -434,7 +482,7 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
         s1 += n1[j];
     }
     const int cinc = wave_scan(csum, lane), i2 = wave_scan(s2, lane), i1 = wave_scan(s1, lane);
-    const int U2 = __shfl(i2, 63, 64), U1 = __shfl(i1, 63, 64);
+    const int U2 = __builtin_amdgcn_readlane(i2, 63), U1 = __builtin_amdgcn_readlane(i1, 63);
     auto xcount = [&](int x) { return 2 * n_mod8(U2, x) + n_mod8(U2 + U1, x) - n_mod8(U2, x); };
     int xstart[8];
     {
@@ -450,10 +498,12 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
     for (int j = 0; j < 4; ++j) {
         const int e = 4 * lane + j;
         if (e < E) {
-            counts[e] = c[j];
-            offsets[e] = off;
             offs[e] = off;
-            for (int m = 0; m < nt[j]; ++m) {
+            if (write) {
+                counts[e] = c[j];
+                offsets[e] = off;
+            }
+            for (int m = 0; write && m < nt[j]; ++m) {
                 const int u = m / 2;
                 int x, pos;  // XCD of the unit and the tile's position in that XCD
                 if (u < n2[j]) {
@@ -481,9 +531,9 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
         r2 += n2[j];
         r1 += n1[j];
     }
-    if (lane == 63) {
+    if (lane == 63) offs[E] = off;
+    if (lane == 63 && write) {
         offsets[E] = off;
-        offs[E] = off;
         hdr[HDR_NTILES] = 2 * U2 + U1;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
@@ -494,92 +544,136 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
     }
 }
 
-// Plan (the scan half of route_build_index_kernel_bf16wts, moe.hpp:1173-1270),
-// one workgroup: reads and clears the block histogram, column-scans it into
-// per-block row bases blkbase[b][e] = offsets[e] + rows of e in blocks < b,
-// and builds counts, offsets and the tile list.
-__global__ __launch_bounds__(1024) void plan_kernel(int32_t *__restrict__ hist, int n_blk, int E,
-                                                   int32_t *__restrict__ counts,
-                                                   int32_t *__restrict__ offsets,
-                                                   int32_t *__restrict__ blkbase,
-                                                   Tile *__restrict__ tiles, int32_t *hdr,
-                                                   int tile_rows) {
+// Exclusive per-expert row offsets from the totals (one wave; lane l owns
+// experts 4 l .. 4 l + 3); offs[E] = all live rows.
+__device__ __forceinline__ void expert_offsets(const int *tot, int *offs, int E, int lane) {
+    int c[4], csum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        c[j] = 4 * lane + j < E ? tot[4 * lane + j] : 0;
+        csum += c[j];
+    }
+    int off = wave_scan(csum, lane) - csum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (4 * lane + j < E) offs[4 * lane + j] = off;
+        off += c[j];
+    }
+    if (lane == 63) offs[E] = off;
+}
+
+// Plan, compact row map and gather in one launch (route_build_index_kernel_bf16wts,
+// moe.hpp:1173-1270, and pack_rows_kernel_bf16_in, moe.hpp:983-1048).
+// Grid (G, n_blk + 1).  Every workgroup of rows b < n_blk:
+//   plan    loads the block histogram (n_blk x (E+1)) into LDS, column-sums
+//           it: per-expert totals, offsets, and the rows of each expert in
+//           blocks < b;
+//   rows    walks block b's slots in rounds of 256 (slot t*K + k ascending,
+//           so rows of an expert come in ascending token order): in-wave rank
+//           from per-expert lane masks, wave counts in LDS, running
+//           per-expert row counters.  Workgroup g = 0 writes the row map;
+//   gather  (xg != nullptr) every workgroup copies the x rows of the round's
+//           slots j with j % G == g into xg[row].  The direct GEMM reads x
+//           through the row map instead and runs with G = 1, no gather.
+// Workgroup (0, n_blk) writes counts, offsets and the tile list; (g > 0,
+// n_blk) exit at once.  The last workgroup to finish clears the histogram for
+// the next call (a counter in the header, reset by that workgroup).
+__global__ __launch_bounds__(256) void index_kernel(
+    int32_t *__restrict__ hist, int n_blk, const int32_t *__restrict__ slot_e,
+    const uint16_t *__restrict__ topk_w, const uint16_t *__restrict__ x, int T, int K, int E,
+    int H, int block_tokens, int tile_rows, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *__restrict__ hdr,
+    int32_t *__restrict__ local_ids, int32_t *__restrict__ row_token, float *__restrict__ row_w,
+    int32_t *__restrict__ row_slot, uint16_t *__restrict__ xg) {
     __shared__ int h[kMaxBlocks * kHistCols];
     __shared__ int tot[kHistCols];
     __shared__ int offs[kMaxExperts + 1];
-    const int tid = threadIdx.x;
-    const int n = n_blk * kHistCols;
-    constexpr int NL = (kMaxBlocks * kHistCols + 1023) / 1024;
-    int v[NL];
-#pragma unroll
-    for (int u = 0; u < NL; ++u) {
-        const int i = tid + 1024 * u;
-        v[u] = i < n ? hist[i] : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < NL; ++u) {
-        const int i = tid + 1024 * u;
-        if (i < n) {
-            h[i] = v[u];
-            hist[i] = 0;
-        }
-    }
-    __syncthreads();
-    if (tid <= E) {  // exclusive scan of column tid over the blocks
-        int s = 0;
-        for (int b = 0; b < n_blk; ++b) {
-            const int c = h[b * kHistCols + tid];
-            h[b * kHistCols + tid] = s;
-            s += c;
-        }
-        tot[tid] = s;
-    }
-    __syncthreads();
-    if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tile_rows, tid);
-    __syncthreads();
-    for (int i = tid; i < n_blk * E; i += 1024) {
-        const int b = i / E, e = i - b * E;
-        blkbase[i] = offs[e] + h[b * kHistCols + e];
-    }
-}
-
-// Compact row map (route_build_index_kernel_bf16wts, moe.hpp:1173-1270) and
-// gather (pack_rows_kernel_bf16_in, moe.hpp:983-1048).  Workgroup (g, b)
-// walks block b's slots in rounds of 256 (slot t*K + k ascending, so rows of
-// an expert come in ascending token order): in-wave rank by shuffles, wave
-// counts in LDS, running per-expert row counters.  Workgroup g = 0 writes the
-// row map; every workgroup copies the x rows of the round's slots j with
-// j % G == g into xg[row].
-__global__ __launch_bounds__(256) void index_gather_kernel(
-    const int32_t *__restrict__ slot_e, const uint16_t *__restrict__ topk_w,
-    const int32_t *__restrict__ blkbase, const uint16_t *__restrict__ x, int T, int K, int E,
-    int H, int block_tokens, int32_t *__restrict__ local_ids, int32_t *__restrict__ row_token,
-    float *__restrict__ row_w, int32_t *__restrict__ row_slot, uint16_t *__restrict__ xg) {
     __shared__ int run[kMaxExperts];
     __shared__ int wcnt[4][kMaxExperts];
     __shared__ int srow[256], stok[256];
+    __shared__ unsigned long long wmask[4][kMaxExperts];
+    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = blockIdx.x, G = gridDim.x, b = blockIdx.y;
+    const bool planner = b == n_blk;
+    if (planner && g > 0) return;
     const int t0 = b * block_tokens;
-    const int nslots = min(block_tokens, T - t0) * K;
+    const int nslots = planner ? 0 : min(block_tokens, T - t0) * K;
     const int s0 = t0 * K;
     const int h8 = H / 8;
-    for (int e = tid; e < E; e += 256) run[e] = blkbase[b * E + e];
+    // the first round's slots, loaded alongside the histogram
+    int e_nx = tid < nslots ? slot_e[s0 + tid] : -1;
+    uint16_t w_nx = tid < nslots ? topk_w[s0 + tid] : 0;
+
+    // ---- plan
+    {
+        // columns 0..E of every block row, up to 16 loads in flight per
+        // thread; element i = tid + 256 u is (row i / nc, column i % nc),
+        // stepped without divisions
+        const int nc = E + 1, n = n_blk * nc;
+        const int dq = 256 / nc, dr = 256 - dq * nc;
+        int bb = tid / nc, c = tid - bb * nc;
+        for (int i0 = tid; i0 < n; i0 += 16 * 256) {
+            int v[16], at[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                at[u] = i0 + 256 * u < n ? bb * kHistCols + c : -1;
+                v[u] = hist[at[u] < 0 ? 0 : at[u]];
+                c += dr;
+                bb += dq;
+                if (c >= nc) {
+                    c -= nc;
+                    ++bb;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (at[u] >= 0) h[at[u]] = v[u];
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c <= E; c += 256) {
+        int pre = 0, sum = 0;
+#pragma unroll 8
+        for (int bb = 0; bb < n_blk; ++bb) {
+            const int v = h[bb * kHistCols + c];
+            pre += bb < b ? v : 0;
+            sum += v;
+        }
+        tot[c] = sum;
+        if (c < E) run[c] = pre;
+    }
+    __syncthreads();
+    if (planner) {
+        if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tile_rows, tid, true);
+    } else {
+        if (tid < 64) expert_offsets(tot, offs, E, tid);
+        __syncthreads();
+        for (int e = tid; e < E; e += 256) run[e] += offs[e];
+    }
+
+    // ---- rows (and gather)
     for (int r0 = 0; r0 < nslots; r0 += 256) {
         for (int e = tid; e < E; e += 256) wcnt[0][e] = wcnt[1][e] = wcnt[2][e] = wcnt[3][e] = 0;
-        __syncthreads();
+        lds_barrier();
         const int s = r0 + tid;
-        const int e = s < nslots ? slot_e[s0 + s] : -1;
-        int rank = 0, same = 0;
-        for (int j = 0; j < 64; ++j) {
-            const int ej = __shfl(e, j, 64);
-            if (ej == e) {
-                ++same;
-                if (j < lane) ++rank;
-            }
+        const int e = e_nx;
+        const uint16_t wt = w_nx;
+        if (r0 + 256 < nslots) {
+            e_nx = s + 256 < nslots ? slot_e[s0 + s + 256] : -1;
+            w_nx = s + 256 < nslots ? topk_w[s0 + s + 256] : 0;
         }
+        // lanes of the wave holding the same expert: each lane ORs its bit
+        // into the wave's mask of its expert (LDS ops of one wave execute in
+        // order, so the read sees every lane's bit)
+        unsigned long long *wm = wmask[wave];
+        for (int e2 = lane; e2 < E; e2 += 64) wm[e2] = 0;
+        if (e >= 0) atomicOr(&wm[e], 1ull << lane);
+        const unsigned long long peers = e >= 0 ? wm[e] : 0ull;
+        const int rank = __popcll(peers & ((1ull << lane) - 1));
+        const int same = __popcll(peers);
         if (e >= 0 && rank == same - 1) wcnt[wave][e] = same;
-        __syncthreads();
+        lds_barrier();
         int row = -1;
         if (e >= 0) {
             row = run[e] + rank;
@@ -591,34 +685,46 @@ __global__ __launch_bounds__(256) void index_gather_kernel(
         if (g == 0 && e >= 0) {
             const int t = (s0 + s) / K;
             row_token[row] = t;
-            row_w[row] = bf2f(topk_w[s0 + s]);
+            row_w[row] = bf2f(wt);
             row_slot[row] = s0 + s;
         }
-        __syncthreads();
+        lds_barrier();
         for (int e2 = tid; e2 < E; e2 += 256)
             run[e2] += wcnt[0][e2] + wcnt[1][e2] + wcnt[2][e2] + wcnt[3][e2];
-        // gather, 4 loads in flight per thread
-        const int cnt = min(256, nslots - r0);
-        const int mine = cnt > g ? (cnt - g + G - 1) / G : 0;
-        const int n = mine * h8;
-        for (int i0 = tid; i0 < n; i0 += 4 * 256) {
-            uint4 v[4];
-            int dst[4], col[4];
+        if (xg != nullptr) {
+            // gather, 4 loads in flight per thread
+            const int cnt = min(256, nslots - r0);
+            const int mine = cnt > g ? (cnt - g + G - 1) / G : 0;
+            const int n = mine * h8;
+            for (int i0 = tid; i0 < n; i0 += 4 * 256) {
+                uint4 v[4];
+                int dst[4], col[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = min(i0 + 256 * u, n - 1);
-                const int m = i / h8, c = i - m * h8;
-                const int j = g + G * m;
-                dst[u] = srow[j];
-                col[u] = 8 * c;
-                v[u] = *reinterpret_cast<const uint4 *>(x + (size_t)stok[j] * H + 8 * c);
+                for (int u = 0; u < 4; ++u) {
+                    const int i = min(i0 + 256 * u, n - 1);
+                    const int m = i / h8, c = i - m * h8;
+                    const int j = g + G * m;
+                    dst[u] = srow[j];
+                    col[u] = 8 * c;
+                    v[u] = *reinterpret_cast<const uint4 *>(x + (size_t)stok[j] * H + 8 * c);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (i0 + 256 * u < n && dst[u] >= 0)
+                        *reinterpret_cast<uint4 *>(xg + (size_t)dst[u] * H + col[u]) = v[u];
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (i0 + 256 * u < n && dst[u] >= 0)
-                    *reinterpret_cast<uint4 *>(xg + (size_t)dst[u] * H + col[u]) = v[u];
         }
-        __syncthreads();
+        lds_barrier();
+    }
+    // the last workgroup to finish (all histogram reads have returned by
+    // now: their values were used above) clears the histogram
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(&hdr[HDR_DONE], 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == G * n_blk;
+    lds_barrier();
+    if (last) {
+        for (int i = tid; i < n_blk * kHistCols; i += 256) hist[i] = 0;
+        if (tid == 0) hdr[HDR_DONE] = 0;
     }
 }
 
@@ -1544,8 +1650,10 @@ struct DSlot {
 
 struct DArgs {
     GemmArgs g;
-    const uint4 *pw;      // packed nibbles of this matrix
-    const uint4 *ps;      // packed scales (16 per row and stage)
+    const uint4 *pw;         // packed nibbles of this matrix
+    const uint4 *ps;         // packed scales (16 per row and stage)
+    const int32_t *a_token;  // non-null: activation row r is g.A row a_token[r] (MLP1 reads x
+                             // through the row map, no gathered copy)
 };
 
 // s_waitcnt vmcnt(N), other counters left alone (gfx9 encoding).
@@ -1763,6 +1871,8 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     // reads are skipped, so their number varies; the waits do not count on it.
     auto issue_lds = [&](int st) {
         DSlot &sl = slots[st % kDSlots];
+        DSlot &sl_next = slots[(st + 1) % kDSlots];
+        const int st_next = min(st + 1, total - 1);
         st = min(st, total - 1);
         Tile tl;
         int nb, j;
@@ -1774,18 +1884,41 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
         // (64 units of 16 B); lane l fetches the unit its LDS position stands
         // for under the row swizzle.  Rows past the tile repeat its last row,
         // k past K the last unit (against zero weights).
-        const char *base = reinterpret_cast<const char *>(a.A + (size_t)tl.row0 * K);
         const int rmax = tl.rows - 1;
         const int rpad = (tl.rows + 15) & ~15;  // rows the MFMAs read
         const int ln = (int)opaque_vgpr((uint32_t)lane);
+        if (d.a_token != nullptr) {
+            // rows by token: this slot's token list (rows past the tile
+            // repeat its last token) was filled one stage ahead
+            if (kDALoads * w < rpad) {
+                u32x4 tk[2];
+                const uint32_t ta = lds_addr(&sl.slot[kDALoads * w]);
+                tk[0] = lds_read_b128_at<0>(ta);
+                tk[1] = lds_read_b128_at<16>(ta);
+                lds_wait(tk[0]);
+                lds_wait(tk[1]);
 #pragma unroll
-        for (int i = 0; i < kDALoads; ++i) {
-            const int q = kDALoads * w + i;
-            if (q < rpad) {
-                const int u = ln ^ (q & 15);
-                const uint32_t off = (uint32_t)min(q, rmax) * (2u * K) +
-                                     2u * (uint32_t)min(j * kDStageK + 8 * u, K - 8);
-                lds_dma16(base + off, &sl.a[64 * q]);
+                for (int i = 0; i < kDALoads; ++i) {
+                    const int q = kDALoads * w + i;
+                    if (q < rpad) {
+                        const int tok = __builtin_amdgcn_readfirstlane((int)tk[i >> 2][i & 3]);
+                        const char *row = reinterpret_cast<const char *>(a.A + (size_t)tok * K);
+                        const int u = ln ^ (q & 15);
+                        lds_dma16(row + 2u * (uint32_t)min(j * kDStageK + 8 * u, K - 8), &sl.a[64 * q]);
+                    }
+                }
+            }
+        } else {
+            const char *base = reinterpret_cast<const char *>(a.A + (size_t)tl.row0 * K);
+#pragma unroll
+            for (int i = 0; i < kDALoads; ++i) {
+                const int q = kDALoads * w + i;
+                if (q < rpad) {
+                    const int u = ln ^ (q & 15);
+                    const uint32_t off = (uint32_t)min(q, rmax) * (2u * K) +
+                                         2u * (uint32_t)min(j * kDStageK + 8 * u, K - 8);
+                    lds_dma16(base + off, &sl.a[64 * q]);
+                }
             }
         }
         // LDS destinations as element addresses (an array argument is not
@@ -1801,7 +1934,16 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
             lds_dma4(a.bias + (size_t)tl.expert * N + min(nb * kDBlockN + 128 * h + 2 * lane, N - 2),
                      &sl.bias[128 * h]);
         } else if (w == 6) {
-            lds_dma4(a.row_slot + tl.row0 + min(lane, rmax), &sl.slot[0]);
+            if (d.a_token == nullptr) {
+                lds_dma4(a.row_slot + tl.row0 + min(lane, rmax), &sl.slot[0]);
+            } else {
+                // row tokens of the next stage's tile (only the slot
+                // being computed meanwhile; its .slot is not read by MLP1)
+                Tile tn;
+                int nbn, jn;
+                lcur.at(a, im, NST, st_next, tn, nbn, jn);
+                lds_dma4(d.a_token + tn.row0 + min(lane, tn.rows - 1), &sl_next.slot[0]);
+            }
         }
     };
 
@@ -1816,6 +1958,16 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     // issue order: lds(0), w(0), w(1); then per iteration s: lds(s + 1), w(s + 2)
+    if (d.a_token != nullptr) {  // row tokens of stage 0
+        if (w == 6) {
+            Tile t0;
+            int nb0, j0;
+            lcur.at(a, im, NST, 0, t0, nb0, j0);
+            lds_dma4(d.a_token + t0.row0 + min(lane, t0.rows - 1), &slots[0].slot[0]);
+        }
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+    }
     issue_lds(0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1977,16 +2129,29 @@ __global__ __launch_bounds__(256) void finalize_kernel(const uint16_t *__restric
     const size_t n = (size_t)T * h8;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
         const int t = (int)(i / h8), c = (int)(i % h8);
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < K; ++j) {
-            if (local_ids[(size_t)t * K + j] < 0) continue;
-            const float w = bf2f(topk_w[(size_t)t * K + j]);
-            const uint4 y = *reinterpret_cast<const uint4 *>(slots + ((size_t)t * K + j) * H + 8 * c);
-            const uint32_t d[4] = {y.x, y.y, y.z, y.w};
+        // every slot's row is loaded up front (a dropped slot's row is
+        // workspace memory, loaded and ignored), then summed in slot order
+        uint4 y[kMaxTopK];
+        float w[kMaxTopK];
+        unsigned live = 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc[2 * q] = __builtin_fmaf(w, __uint_as_float(d[q] << 16), acc[2 * q]);
-                acc[2 * q + 1] = __builtin_fmaf(w, __uint_as_float(d[q] & 0xffff0000u), acc[2 * q + 1]);
+        for (int j = 0; j < kMaxTopK; ++j) {
+            if (j < K) {
+                live |= (local_ids[(size_t)t * K + j] >= 0 ? 1u : 0u) << j;
+                w[j] = bf2f(topk_w[(size_t)t * K + j]);
+                y[j] = *reinterpret_cast<const uint4 *>(slots + ((size_t)t * K + j) * H + 8 * c);
+            }
+        }
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+            if (j < K && ((live >> j) & 1u)) {
+                const uint32_t d[4] = {y[j].x, y[j].y, y[j].z, y[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    acc[2 * q] = __builtin_fmaf(w[j], __uint_as_float(d[q] << 16), acc[2 * q]);
+                    acc[2 * q + 1] = __builtin_fmaf(w[j], __uint_as_float(d[q] & 0xffff0000u), acc[2 * q + 1]);
+                }
             }
         }
         uint4 *po = reinterpret_cast<uint4 *>(out + (size_t)t * H + 8 * c);
@@ -2110,7 +2275,7 @@ constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SM
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 struct Ptrs {
-    int32_t *hdr, *hist, *blkbase, *counts, *offsets, *topk_i, *slot_e, *local_ids, *row_token;
+    int32_t *hdr, *hist, *counts, *offsets, *topk_i, *slot_e, *local_ids, *row_token;
     Tile *tiles;
     uint16_t *logits, *topk_w, *act, *slots, *xg;
     int32_t *row_slot;
@@ -2122,7 +2287,6 @@ Ptrs ws_ptrs(const WsLayout &L, void *ws) {
     Ptrs p;
     p.hdr = (int32_t *)(b + L.hdr);
     p.hist = (int32_t *)(b + L.hist);
-    p.blkbase = (int32_t *)(b + L.blkbase);
     p.slot_e = (int32_t *)(b + L.slot_e);
     p.counts = (int32_t *)(b + L.counts);
     p.offsets = (int32_t *)(b + L.offsets);
@@ -2188,7 +2352,7 @@ void launch_route_tb(int ee, const gptoss_moe_shape *s, const gptoss_moe_weights
 
 int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                  int T, const int32_t *fi, const uint16_t *fw, const Ptrs &p, hipStream_t st,
-                 int tile_rows, Marks *mk = nullptr) {
+                 int tile_rows, bool gather, Marks *mk = nullptr) {
     int nthreads_ref = 1;
     while (nthreads_ref < s->n_experts) nthreads_ref <<= 1;
     nthreads_ref = nthreads_ref < 64 ? 64 : (nthreads_ref > 512 ? 512 : nthreads_ref);
@@ -2209,14 +2373,14 @@ int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const u
         launch_route_tb<4>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
     else
         launch_route_tb<1>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, p.hist, n_blk, E, p.counts,
-                       p.offsets, p.blkbase, p.tiles, p.hdr, tile_rows);
     if (mk) mk->mark(st);
     int G = 8 * device_cus() / n_blk;
     G = G < 1 ? 1 : (G > 256 ? 256 : G);
-    hipLaunchKernelGGL(index_gather_kernel, dim3(G, n_blk), dim3(256), 0, st, p.slot_e, p.topk_w,
-                       p.blkbase, x, T, s->top_k, E, s->hidden, bt, p.local_ids, p.row_token,
-                       p.row_w, p.row_slot, p.xg);
+    if (!gather) G = 1;
+    hipLaunchKernelGGL(index_kernel, dim3(G, n_blk + 1), dim3(256), 0, st, p.hist, n_blk, p.slot_e,
+                       p.topk_w, x, T, s->top_k, E, s->hidden, bt, tile_rows, p.counts, p.offsets,
+                       p.tiles, p.hdr, p.local_ids, p.row_token, p.row_w, p.row_slot,
+                       gather ? p.xg : nullptr);
     if (mk) mk->mark(st);
     return hip_status(hipGetLastError());
 }
@@ -2283,13 +2447,15 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     const GemmPath path = gemm_path(s, w, T, flags);
     const bool large = path == PATH_LARGE_M, direct = path == PATH_DIRECT;
     const PackLayout PL = pack_layout(*s);
+    GemmArgs a1x = a1;  // the direct GEMM reads x through the row map
+    a1x.A = x;
     if (large)
         hipLaunchKernelGGL(large_m_gemm_kernel<true>, dim3(cap), dim3(kLWaves * 64), 0, st, a1,
                            p.counts, p.offsets, s->n_experts);
     else if (direct)
         hipLaunchKernelGGL(direct_gemm_kernel<true>, dim3(cap), dim3(kDWaves * 64), 0, st,
-                           DArgs{a1, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
-                                 reinterpret_cast<const uint4 *>(w->packed + PL.s1)});
+                           DArgs{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
+                                 reinterpret_cast<const uint4 *>(w->packed + PL.s1), p.row_token});
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a1);
     if (mk) mk->mark(st);
@@ -2309,7 +2475,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     else if (direct)
         hipLaunchKernelGGL(direct_gemm_kernel<false>, dim3(cap), dim3(kDWaves * 64), 0, st,
                            DArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
-                                 reinterpret_cast<const uint4 *>(w->packed + PL.s2)});
+                                 reinterpret_cast<const uint4 *>(w->packed + PL.s2), nullptr});
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a2);
     if (mk) mk->mark(st);
@@ -2372,7 +2538,7 @@ int gptoss_moe_route(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
     if (!x_norm || !aligned16(x_norm)) return GPTOSS_MOE_ERR_INVALID_ARG;
     const WsLayout L = ws_layout(*shape, max_tokens);
     return launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w,
-                        ws_ptrs(L, workspace), stream, gemm_tile_rows(shape, w, n_tokens, 0));
+                        ws_ptrs(L, workspace), stream, gemm_tile_rows(shape, w, n_tokens, 0), false);
 }
 
 int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
@@ -2389,7 +2555,8 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
-                      gemm_tile_rows(shape, w, n_tokens, flags));
+                      gemm_tile_rows(shape, w, n_tokens, flags),
+                      gemm_path(shape, w, n_tokens, flags) != PATH_DIRECT);
     if (rc) return rc;
     return launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream);
 }
@@ -2413,7 +2580,8 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
     const Ptrs p = ws_ptrs(L, workspace);
     mk.mark(stream);
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
-                      gemm_tile_rows(shape, w, n_tokens, flags), &mk);
+                      gemm_tile_rows(shape, w, n_tokens, flags),
+                      gemm_path(shape, w, n_tokens, flags) != PATH_DIRECT, &mk);
     if (!rc) rc = launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream, &mk);
     if (!rc) rc = hip_status(hipEventSynchronize(mk.ev[5]));
     for (int i = 0; i < 5 && !rc; ++i)

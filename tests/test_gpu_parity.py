@@ -277,6 +277,31 @@ def test_forward_repeatable_and_residual(gpu):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("path", ["auto", "small"])
+def test_forward_sequence_of_batch_sizes(gpu, path):
+    """One workspace, batches of changing size in a row: the routing
+    histogram is cleared by each call for the next (more than one histogram
+    block at 1000 tokens; the LDS-staged path also gathers with several
+    workgroups per block)."""
+    import gptoss_moe
+    d = synth.make_data("c1_20b_decode", tokens=1000)
+    c = d.cfg
+    layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
+    x = _dev(d.x, gpu)
+    for n in (1000, 17, 300, 1000, 64):
+        out = layer.forward(x[:n], path=path)
+        v = layer.views(n)
+        lg = oracle.router_logits(d.x[:n], d.router_w)
+        ti, _ = oracle.topk_softmax(lg, d.router_b, c.top_k)
+        assert np.array_equal(v["topk_i"], ti), f"{n} tokens: topk_i differs"
+        ref = oracle.route_index(ti, v["topk_w"], c.n_experts)
+        for k in ("counts", "offsets", "local_ids", "row_token", "row_weight"):
+            assert np.array_equal(v[k], ref[k]), f"{n} tokens: {k} differs"
+    rows = np.arange(0, 64, 5)  # the last call's tokens are rows 0..63 of d.x
+    ref = oracle.moe_forward(d, forced=False, rows=rows)
+    assert_close(_host16(out)[rows], ref["e_agg"], "c1 64 tokens after a sequence")
+
+
 @pytest.mark.parametrize("tokens", [1, 3, 17])
 def test_forward_small_batches(gpu, tokens):
     d = synth.make_data("c1_20b_decode", tokens=tokens)
