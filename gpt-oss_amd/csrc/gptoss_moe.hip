@@ -30,6 +30,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;  // register-friendly 16 bytes
+typedef __attribute__((ext_vector_type(8))) int i32x8;
 
 constexpr int kWave = 64;
 constexpr int kMaxExperts = 256;
@@ -75,7 +76,7 @@ __device__ __forceinline__ uint32_t zero_scale_fix(uint32_t q, uint32_t e) {
 // ------------------------------------------------------- workspace map --
 struct WsLayout {
     size_t hdr, hist, counts, offsets, tiles, logits, topk_i, topk_w, slot_e, local_ids,
-        row_token, row_w, row_slot, xg, act, slots, total;
+        row_token, row_w, row_slot, xg, act, slots, xq, xqs, aq, aqs, total;
     int max_tiles;
 };
 
@@ -124,6 +125,12 @@ WsLayout ws_layout(const gptoss_moe_shape &s, int max_tokens) {
     L.xg = take(P * (size_t)s.hidden * 2);
     L.act = take(P * (size_t)s.intermediate * 2);
     L.slots = take(P * (size_t)s.hidden * 2);
+    // MXFP8 activations of the scaled-MFMA variant (x per token, act per row)
+    const size_t KSH = (size_t)(s.hidden + 511) / 512, KSD = (size_t)(s.intermediate + 511) / 512;
+    L.xq = take(T * KSH * 1024);
+    L.xqs = take(T * KSH * 32);
+    L.aq = take(P * KSD * 1024);
+    L.aqs = take(P * KSD * 32);
     L.total = o;
     return L;
 }
@@ -1566,10 +1573,16 @@ PackLayout pack_layout(const gptoss_moe_shape &s) {
 __device__ __forceinline__ int packed_src_row(int pr, bool mlp1) {
     return mlp1 ? (pr & ~31) + 2 * (pr & 15) + ((pr >> 4) & 1) : pr;
 }
+// Scaled-MFMA order (fmt 1, for v_mfma_scale_f32_16x16x128_f8f6f4, whose B
+// operand lane (n, g) holds k = 32 g .. 32 g + 31 of column n, low nibble
+// first, and whose scale operand lane (n, g) the e8m0 of that 32-k group):
+//   nibbles: same blocks, lane (n, g) = row bytes 64 kp + 16 g .. + 15;
+//   scales:  per (e, ct, kq) 64 lanes x 4 B, lane (n, g) byte b = the e8m0 of
+//            row 16 ct + n, k group 16 kq + 4 b + g (k step 4 kq + b).
 // One thread per packed dword (nibbles) or byte (scales).
 __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ wq,
                                                   const uint8_t *__restrict__ ws, int N, int K,
-                                                  int E, int mlp1, uint32_t *__restrict__ pw,
+                                                  int E, int mlp1, int fmt, uint32_t *__restrict__ pw,
                                                   uint8_t *__restrict__ ps) {
     const int KP = (K + 127) / 128, KQ = (K + 511) / 512, CT = N / 16, KS = K / 32;
     const size_t nw = (size_t)E * CT * KP * 256;  // dwords
@@ -1584,14 +1597,17 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
             const int ct = (int)(r % CT);
             const int e = (int)(r / CT);
             const int row = packed_src_row(16 * ct + (lane & 15), mlp1 != 0);
-            const int byte = 64 * kp + 16 * q + 4 * (lane >> 4);
+            const int byte = fmt == 0 ? 64 * kp + 16 * q + 4 * (lane >> 4)
+                                      : 64 * kp + 16 * (lane >> 4) + 4 * q;
             uint32_t v = 0;
             if (byte < K / 2)
                 v = *reinterpret_cast<const uint32_t *>(wq + ((size_t)e * N + row) * (K / 2) + byte);
             pw[i] = v;
         } else {
             const size_t b = i - nw;
-            const int gi = (int)(b & 15), n = (int)((b >> 4) & 15);
+            // fmt 0: byte (n, gi) = row n, group gi; fmt 1: lane (n, g), byte bb -> group 4 bb + g
+            const int n = fmt == 0 ? (int)((b >> 4) & 15) : (int)((b >> 2) & 15);
+            const int gi = fmt == 0 ? (int)(b & 15) : (int)(4 * (b & 3) + ((b >> 6) & 3));
             size_t r = b >> 8;
             const int kq = (int)(r % KQ);
             r /= KQ;
@@ -1644,8 +1660,10 @@ constexpr int kDALoads = kDTileRows * kDUnits / 64 / kDWaves;  // 1 KB activatio
 struct DSlot {
     uint4 a[kDTileRows * kDUnits];  // tile row r, 16-byte unit u at r * 64 + (u ^ (r & 15))
     uint4 sc[kDBlockN];             // e8m0 of the stage: column tile c, row n at 16 c + n
+                                    // (scaled-MFMA variant: tile c's 64 lane dwords)
+    uint4 as[2 * kDTileRows];       // variant: MXFP8 scales of tile row r, hi at 2 r, lo at 2 r + 1
     uint16_t bias[kDBlockN];        // bias of block rows 0..255 (weight-row order)
-    int32_t slot[kDTileRows];       // token-order slot of tile row r (MLP2)
+    int32_t slot[kDTileRows];       // token-order slot of tile row r (MLP2), or row tokens (MLP1)
 };
 
 struct DArgs {
@@ -1654,6 +1672,7 @@ struct DArgs {
     const uint4 *ps;         // packed scales (16 per row and stage)
     const int32_t *a_token;  // non-null: activation row r is g.A row a_token[r] (MLP1 reads x
                              // through the row map, no gathered copy)
+    const uint8_t *aqs;      // variant: MXFP8 activation scales, rows of ceil(K/512) * 32 B
 };
 
 // s_waitcnt vmcnt(N), other counters left alone (gfx9 encoding).
@@ -1681,6 +1700,12 @@ template <int OFF>
 __device__ __forceinline__ u32x4 lds_read_b128_at(uint32_t addr) {
     u32x4 v;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_b32_at(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
     return v;
 }
 __device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
@@ -1764,6 +1789,100 @@ __device__ __forceinline__ void direct_stage(const DSlot &sl, const uint4 (&w)[2
     }
 }
 
+// Block-scaled FP4 MFMA variant: one stage (512 k) of a wave's 2 column tiles
+// with v_mfma_scale_f32_16x16x128_f8f6f4 (A = MXFP8 activations, B = the
+// packed E2M1 weights, both e8m0-scaled per 32 k).  Operand order of one
+// 128-k step kp: A lane (i, g) = row i, bytes 32 g .. 32 g + 31 of the
+// step's 128-byte block (k 16 g .. + 15, 64 + 16 g .. + 15), its scale =
+// byte kp of dword g of the row's stage scales; B lane (n, g) = the 16 bytes
+// of chunk kp (k 32 g .. + 31 of row n), scale = byte kp of its lane dword.
+// C as for the bf16 MFMA: lane (n, g) holds rows 4 g .. 4 g + 3 of column n.
+// Two terms: a second MFMA per step adds the lo codes at their own scale.
+template <int KP, int MT, int kAq>
+__device__ __forceinline__ void fp4_kstep(uint32_t abase, uint32_t c0, uint32_t c1,
+                                          const uint4 (&w)[2][kDChunks], const uint32_t (&sb)[2],
+                                          const uint32_t (&sah)[MT], const uint32_t (&sal)[MT],
+                                          f32x4 (&acc)[4][2]) {
+    // units 8 KP + 2 g and + 1 of the row under the LDS swizzle (u ^ (row & 15))
+    const uint32_t a0 = abase + 16u * ((8u * KP) ^ c0), a1 = abase + 16u * ((8u * KP) ^ c1);
+    constexpr int G = 16 * kDUnits * 16;  // bytes per 16-row group
+    u32x4 h0[MT], h1[MT], l0[MT], l1[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        h0[m] = m == 0 ? lds_read_b128_at<0>(a0) : m == 1 ? lds_read_b128_at<G>(a0)
+              : m == 2 ? lds_read_b128_at<2 * G>(a0) : lds_read_b128_at<3 * G>(a0);
+        h1[m] = m == 0 ? lds_read_b128_at<0>(a1) : m == 1 ? lds_read_b128_at<G>(a1)
+              : m == 2 ? lds_read_b128_at<2 * G>(a1) : lds_read_b128_at<3 * G>(a1);
+        if constexpr (kAq == 2) {
+            l0[m] = m == 0 ? lds_read_b128_at<512>(a0) : m == 1 ? lds_read_b128_at<G + 512>(a0)
+                  : m == 2 ? lds_read_b128_at<2 * G + 512>(a0) : lds_read_b128_at<3 * G + 512>(a0);
+            l1[m] = m == 0 ? lds_read_b128_at<512>(a1) : m == 1 ? lds_read_b128_at<G + 512>(a1)
+                  : m == 2 ? lds_read_b128_at<2 * G + 512>(a1) : lds_read_b128_at<3 * G + 512>(a1);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        lds_wait(h0[m]);
+        lds_wait(h1[m]);
+        if constexpr (kAq == 2) {
+            lds_wait(l0[m]);
+            lds_wait(l1[m]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint4 bv = w[t][KP];
+        const i32x8 b = {(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const i32x8 ah = {(int)h0[m][0], (int)h0[m][1], (int)h0[m][2], (int)h0[m][3],
+                              (int)h1[m][0], (int)h1[m][1], (int)h1[m][2], (int)h1[m][3]};
+            acc[m][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah, b, acc[m][t], 0, 4, KP,
+                                                                         (int)sah[m], KP, (int)sb[t]);
+            if constexpr (kAq == 2) {
+                const i32x8 al = {(int)l0[m][0], (int)l0[m][1], (int)l0[m][2], (int)l0[m][3],
+                                  (int)l1[m][0], (int)l1[m][1], (int)l1[m][2], (int)l1[m][3]};
+                acc[m][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, b, acc[m][t], 0, 4, KP,
+                                                                             (int)sal[m], KP, (int)sb[t]);
+            }
+        }
+    }
+}
+
+template <int MT, int kAq>
+__device__ __forceinline__ void fp4_stage(const DSlot &sl, const uint4 (&w)[2][kDChunks],
+                                          f32x4 (&acc)[4][2]) {
+    const int lane = threadIdx.x & 63, n_l = lane & 15, g = lane >> 4;
+    const int wave = threadIdx.x >> 6;
+    uint32_t sb[2], sah[MT], sal[MT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) sb[t] = lds_read_b32(lds_addr(&sl.sc[16 * (2 * wave + t)]) + 4u * lane);
+    // scales of row 16 m + n_l: hi dword g at 32 row + 4 g, lo 16 bytes on
+    const uint32_t asb = opaque_vgpr(lds_addr(&sl.as[0])) + 32u * n_l + 4u * g;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        sah[m] = m == 0 ? lds_read_b32_at<0>(asb) : m == 1 ? lds_read_b32_at<512>(asb)
+               : m == 2 ? lds_read_b32_at<1024>(asb) : lds_read_b32_at<1536>(asb);
+        sal[m] = 0;
+        if constexpr (kAq == 2)
+            sal[m] = m == 0 ? lds_read_b32_at<16>(asb) : m == 1 ? lds_read_b32_at<528>(asb)
+                   : m == 2 ? lds_read_b32_at<1040>(asb) : lds_read_b32_at<1552>(asb);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) lds_wait(sb[t]);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        lds_wait(sah[m]);
+        if constexpr (kAq == 2) lds_wait(sal[m]);
+    }
+    const uint32_t abase = opaque_vgpr(lds_addr(sl.a)) + 1024u * n_l;
+    const uint32_t c0 = (uint32_t)((2 * g) ^ n_l), c1 = (uint32_t)((2 * g + 1) ^ n_l);
+    fp4_kstep<0, MT, kAq>(abase, c0, c1, w, sb, sah, sal, acc);
+    fp4_kstep<1, MT, kAq>(abase, c0, c1, w, sb, sah, sal, acc);
+    fp4_kstep<2, MT, kAq>(abase, c0, c1, w, sb, sah, sal, acc);
+    fp4_kstep<3, MT, kAq>(abase, c0, c1, w, sb, sah, sal, acc);
+}
+
 template <int MT, bool kMlp1>
 __device__ __forceinline__ void direct_epilogue(const GemmArgs &a, const DSlot &sl, const Tile &tl,
                                                 int nb, const f32x4 (&acc)[4][2]) {
@@ -1825,7 +1944,9 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs &a, const DSlot &
     }
 }
 
-template <bool kMlp1>
+// kAq = 0: bf16 MFMA on dequantised weights (the default path); 1 / 2: the
+// block-scaled FP4 MFMA variant on MXFP8 activations (one / two terms).
+template <bool kMlp1, int kAq>
 __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     __shared__ DSlot slots[kDSlots];
     const GemmArgs &a = d.g;
@@ -1841,6 +1962,7 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
     const int lane = threadIdx.x & 63;
     const int N = a.N, K = a.K;
     const int CT = N / 16, KP = (K + 127) / 128, KQ = (K + 511) / 512;
+    const size_t AQP = (size_t)KQ * 1024;  // variant: bytes per MXFP8 activation row
     uint4 wr[kDDepth][2][kDChunks];
     StepCursor wcur, lcur, ccur;
 #ifdef GPTOSS_TRACE
@@ -1902,10 +2024,26 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
                     const int q = kDALoads * w + i;
                     if (q < rpad) {
                         const int tok = __builtin_amdgcn_readfirstlane((int)tk[i >> 2][i & 3]);
-                        const char *row = reinterpret_cast<const char *>(a.A + (size_t)tok * K);
                         const int u = ln ^ (q & 15);
-                        lds_dma16(row + 2u * (uint32_t)min(j * kDStageK + 8 * u, K - 8), &sl.a[64 * q]);
+                        if constexpr (kAq != 0) {
+                            const char *row = reinterpret_cast<const char *>(a.A) + (size_t)tok * AQP;
+                            lds_dma16(row + 1024u * (uint32_t)j + 16u * (uint32_t)u, &sl.a[64 * q]);
+                        } else {
+                            const char *row = reinterpret_cast<const char *>(a.A + (size_t)tok * K);
+                            lds_dma16(row + 2u * (uint32_t)min(j * kDStageK + 8 * u, K - 8), &sl.a[64 * q]);
+                        }
                     }
+                }
+            }
+        } else if constexpr (kAq != 0) {
+            const char *base = reinterpret_cast<const char *>(a.A) + (size_t)tl.row0 * AQP;
+#pragma unroll
+            for (int i = 0; i < kDALoads; ++i) {
+                const int q = kDALoads * w + i;
+                if (q < rpad) {
+                    const int u = ln ^ (q & 15);
+                    lds_dma16(base + (size_t)min(q, rmax) * AQP + 1024u * (uint32_t)j + 16u * (uint32_t)u,
+                              &sl.a[64 * q]);
                 }
             }
         } else {
@@ -1943,6 +2081,21 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
                 int nbn, jn;
                 lcur.at(a, im, NST, st_next, tn, nbn, jn);
                 lds_dma4(d.a_token + tn.row0 + min(lane, tn.rows - 1), &sl_next.slot[0]);
+            }
+        } else if (kAq != 0) {
+            // wave 7: MXFP8 scales of the stage, 32 B per row (hi, lo);
+            // load h: rows 32 h + (l >> 1), half l & 1
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int q = min(32 * h + (lane >> 1), rmax);
+                int rowid = tl.row0 + q;
+                if (d.a_token != nullptr) {  // this slot's row tokens (filled one stage ahead)
+                    uint32_t tk = lds_read_b32(lds_addr(&sl.slot[0]) + 4u * (uint32_t)q);
+                    lds_wait(tk);
+                    rowid = (int)tk;
+                }
+                lds_dma16(d.aqs + (size_t)rowid * (AQP / 32) + 32u * (uint32_t)j + 16u * (uint32_t)(lane & 1),
+                          &sl.as[64 * h]);
             }
         }
     };
@@ -2027,10 +2180,17 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
                     }
                 const DSlot &sl = slots[s % kDSlots];
                 const int mt = (tl.rows + 15) >> 4;
-                if (mt <= 1) direct_stage<1>(sl, wv, acc);
-                else if (mt == 2) direct_stage<2>(sl, wv, acc);
-                else if (mt == 3) direct_stage<3>(sl, wv, acc);
-                else direct_stage<4>(sl, wv, acc);
+                if constexpr (kAq != 0) {
+                    if (mt <= 1) fp4_stage<1, kAq>(sl, wv, acc);
+                    else if (mt == 2) fp4_stage<2, kAq>(sl, wv, acc);
+                    else if (mt == 3) fp4_stage<3, kAq>(sl, wv, acc);
+                    else fp4_stage<4, kAq>(sl, wv, acc);
+                } else {
+                    if (mt <= 1) direct_stage<1>(sl, wv, acc);
+                    else if (mt == 2) direct_stage<2>(sl, wv, acc);
+                    else if (mt == 3) direct_stage<3>(sl, wv, acc);
+                    else direct_stage<4>(sl, wv, acc);
+                }
                 DTR(tc)
                 if (j == NST - 1) {
                     if (mt <= 1) direct_epilogue<1, kMlp1>(a, sl, tl, nb, acc);
@@ -2113,6 +2273,78 @@ __global__ __launch_bounds__(256) void quantize_mxfp4_kernel(const float *__rest
             const int eb = exp_scale + 127;
             scales[blk] = (uint8_t)(eb < 0 ? 0 : (eb > 255 ? 255 : eb));
         }
+    }
+}
+
+// MXFP8 activations of the block-scaled FP4 MFMA variant (no counterpart in
+// the reference).  Per 32-k group: e = floor(log2 max|x|) - 7, clamped to
+// [-123, 120] (0 for an all-zero group); hi = e4m3(x 2^-e), and with two
+// terms lo = e4m3((x 2^-e - hi) 16), both round to nearest even; e8m0
+// scales e + 127 (hi), e + 123 (lo).  Row layout: ceil(K/512) stages of 1 KB
+// (hi 512 B, lo 512 B); in a stage, byte 128 kp + 32 g + 16 h + j is
+// k = 128 kp + 64 h + 16 g + j (the MFMA's A-operand order), k >= K zero.
+// Scales per row and stage: hi 16 B then lo 16 B, byte 4 g + b = 32-k group
+// 4 b + g.  One wave per (row, stage): lane l takes k = 8 l .. 8 l + 7 of the
+// stage; a 32-k group is a lane quad.  Rows at or past *live_rows (when
+// given) are skipped.
+__global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t *__restrict__ x, int rows,
+                                                          int K, int terms,
+                                                          const int32_t *__restrict__ live_rows,
+                                                          uint8_t *__restrict__ q,
+                                                          uint8_t *__restrict__ qs) {
+    const int lane = threadIdx.x & 63;
+    const int KS = (K + 511) / 512;
+    const int64_t wv = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+    const int nrows = live_rows != nullptr ? min(rows, *live_rows) : rows;
+    if (wv >= (int64_t)nrows * KS) return;
+    const int row = (int)(wv / KS), j = (int)(wv - (int64_t)row * KS);
+    const int k0 = 512 * j + 8 * lane;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (k0 < K) v = *reinterpret_cast<const uint4 *>(x + (size_t)row * K + k0);
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(d[i] << 16);
+        f[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(f[i]));
+    am = fmaxf(am, xor16<1>(am));
+    am = fmaxf(am, xor16<2>(am));
+    int e = 0;
+    if (am > 0.f) e = min(max((int)((__float_as_uint(am) >> 23) & 255u) - 127 - 7, -123), 120);
+    const float sc = __uint_as_float((uint32_t)(127 - e) << 23);  // 2^-e
+    uint32_t hi[2] = {0u, 0u}, lo[2] = {0u, 0u};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float vs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vs[i] = f[4 * h + i] * sc;
+        uint32_t c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vs[0], vs[1], 0, false);
+        c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vs[2], vs[3], (int)c, true);
+        hi[h] = c;
+        if (terms == 2) {
+            const float r[4] = {(vs[0] - __builtin_amdgcn_cvt_f32_fp8((int)c, 0)) * 16.f,
+                                (vs[1] - __builtin_amdgcn_cvt_f32_fp8((int)c, 1)) * 16.f,
+                                (vs[2] - __builtin_amdgcn_cvt_f32_fp8((int)c, 2)) * 16.f,
+                                (vs[3] - __builtin_amdgcn_cvt_f32_fp8((int)c, 3)) * 16.f};
+            uint32_t cl = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+            cl = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], (int)cl, true);
+            lo[h] = cl;
+        }
+    }
+    // lane l: k step l / 16, g = (l % 8) / 2, h = (l % 16) / 8, bytes 8 (l % 2) .. + 7
+    const int pos = 128 * (lane >> 4) + 32 * ((lane & 7) >> 1) + 16 * ((lane >> 3) & 1) + 8 * (lane & 1);
+    uint8_t *qr = q + ((size_t)row * KS + j) * 1024;
+    *reinterpret_cast<uint2 *>(qr + pos) = make_uint2(hi[0], hi[1]);
+    *reinterpret_cast<uint2 *>(qr + 512 + pos) = make_uint2(lo[0], lo[1]);
+    if ((lane & 3) == 0) {
+        const int grp = lane >> 2;
+        uint8_t *sr = qs + ((size_t)row * KS + j) * 32 + 4 * (grp & 3) + (grp >> 2);
+        sr[0] = (uint8_t)(e + 127);
+        sr[16] = (uint8_t)(e + 123);
     }
 }
 
@@ -2270,7 +2502,8 @@ bool shape_ok(const gptoss_moe_shape *s) {
 }
 
 constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SMALL_M_GEMM |
-                               GPTOSS_MOE_FLAG_LARGE_M_GEMM;
+                               GPTOSS_MOE_FLAG_LARGE_M_GEMM | GPTOSS_MOE_FLAG_FP4_MFMA |
+                               GPTOSS_MOE_FLAG_FP8_ACT;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -2278,6 +2511,7 @@ struct Ptrs {
     int32_t *hdr, *hist, *counts, *offsets, *topk_i, *slot_e, *local_ids, *row_token;
     Tile *tiles;
     uint16_t *logits, *topk_w, *act, *slots, *xg;
+    uint8_t *xq, *xqs, *aq, *aqs;
     int32_t *row_slot;
     float *row_w;
 };
@@ -2301,6 +2535,10 @@ Ptrs ws_ptrs(const WsLayout &L, void *ws) {
     p.act = (uint16_t *)(b + L.act);
     p.xg = (uint16_t *)(b + L.xg);
     p.slots = (uint16_t *)(b + L.slots);
+    p.xq = (uint8_t *)(b + L.xq);
+    p.xqs = (uint8_t *)(b + L.xqs);
+    p.aq = (uint8_t *)(b + L.aq);
+    p.aqs = (uint8_t *)(b + L.aqs);
     return p;
 }
 
@@ -2400,8 +2638,9 @@ bool use_large_m(const gptoss_moe_shape *s, int T, unsigned flags) {
 // GEMM path of a forward call.  With packed weights the direct GEMM runs at
 // every batch size (it outruns the large-M path on prefill too) unless a
 // flag forces another path; without them the small-M / large-M choice above.
-enum GemmPath { PATH_SMALL_M, PATH_LARGE_M, PATH_DIRECT };
+enum GemmPath { PATH_SMALL_M, PATH_LARGE_M, PATH_DIRECT, PATH_FP4 };
 GemmPath gemm_path(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, unsigned flags) {
+    if (flags & GPTOSS_MOE_FLAG_FP4_MFMA) return PATH_FP4;
     if (flags & GPTOSS_MOE_FLAG_LARGE_M_GEMM) return use_large_m(s, T, flags) ? PATH_LARGE_M : PATH_SMALL_M;
     if (w->packed != nullptr && !(flags & GPTOSS_MOE_FLAG_SMALL_M_GEMM)) return PATH_DIRECT;
     return use_large_m(s, T, flags) ? PATH_LARGE_M : PATH_SMALL_M;
@@ -2410,7 +2649,8 @@ GemmPath gemm_path(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T
 // Rows per tile of the tile list: the direct GEMM takes whole decode experts,
 // up to 64 rows; the LDS-staged GEMM 32 (the large-M GEMM builds its own).
 int gemm_tile_rows(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, unsigned flags) {
-    return gemm_path(s, w, T, flags) == PATH_DIRECT ? kDTileRows : kTileRows;
+    const GemmPath p = gemm_path(s, w, T, flags);
+    return p == PATH_DIRECT || p == PATH_FP4 ? kDTileRows : kTileRows;
 }
 
 // Expert weights and flags of a forward call.
@@ -2418,9 +2658,24 @@ int check_experts(const gptoss_moe_weights *w, unsigned flags) {
     if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
     if (!w->w1 || !w->w1_scales || !w->b1 || !w->w2 || !w->w2_scales || !w->b2)
         return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (!aligned16(w->w1) || !aligned16(w->w2) || !aligned16(w->packed))
+    if (!aligned16(w->w1) || !aligned16(w->w2) || !aligned16(w->packed) || !aligned16(w->packed_fp4))
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    if ((flags & GPTOSS_MOE_FLAG_FP4_MFMA) && w->packed_fp4 == nullptr) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if ((flags & GPTOSS_MOE_FLAG_FP8_ACT) && !(flags & GPTOSS_MOE_FLAG_FP4_MFMA))
+        return GPTOSS_MOE_ERR_INVALID_ARG;
+    if ((flags & GPTOSS_MOE_FLAG_FP4_MFMA) &&
+        (flags & (GPTOSS_MOE_FLAG_SMALL_M_GEMM | GPTOSS_MOE_FLAG_LARGE_M_GEMM)))
         return GPTOSS_MOE_ERR_INVALID_ARG;
     return GPTOSS_MOE_OK;
+}
+
+void launch_quantize_act(const uint16_t *x, int rows, int K, int terms, const int32_t *live_rows,
+                         uint8_t *q, uint8_t *qs, hipStream_t st) {
+    const int64_t waves = (int64_t)rows * ((K + 511) / 512);
+    const int grid = (int)((waves + 3) / 4);
+    if (grid > 0)
+        hipLaunchKernelGGL(quantize_act_kernel, dim3(grid), dim3(256), 0, st, x, rows, K, terms,
+                           live_rows, q, qs);
 }
 
 int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
@@ -2445,7 +2700,8 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a1.limit = s->swiglu_limit;
     a1.alpha = s->swiglu_alpha;
     const GemmPath path = gemm_path(s, w, T, flags);
-    const bool large = path == PATH_LARGE_M, direct = path == PATH_DIRECT;
+    const bool large = path == PATH_LARGE_M, direct = path == PATH_DIRECT, fp4 = path == PATH_FP4;
+    const int terms = (flags & GPTOSS_MOE_FLAG_FP8_ACT) ? 1 : 2;
     const PackLayout PL = pack_layout(*s);
     GemmArgs a1x = a1;  // the direct GEMM reads x through the row map
     a1x.A = x;
@@ -2453,9 +2709,21 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         hipLaunchKernelGGL(large_m_gemm_kernel<true>, dim3(cap), dim3(kLWaves * 64), 0, st, a1,
                            p.counts, p.offsets, s->n_experts);
     else if (direct)
-        hipLaunchKernelGGL(direct_gemm_kernel<true>, dim3(cap), dim3(kDWaves * 64), 0, st,
+        hipLaunchKernelGGL((direct_gemm_kernel<true, 0>), dim3(cap), dim3(kDWaves * 64), 0, st,
                            DArgs{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
-                                 reinterpret_cast<const uint4 *>(w->packed + PL.s1), p.row_token});
+                                 reinterpret_cast<const uint4 *>(w->packed + PL.s1), p.row_token,
+                                 nullptr});
+    else if (fp4) {
+        launch_quantize_act(x, T, H, terms, nullptr, p.xq, p.xqs, st);
+        GemmArgs aq1 = a1;
+        aq1.A = reinterpret_cast<const uint16_t *>(p.xq);
+        const DArgs da{aq1, reinterpret_cast<const uint4 *>(w->packed_fp4 + PL.w1),
+                       reinterpret_cast<const uint4 *>(w->packed_fp4 + PL.s1), p.row_token, p.xqs};
+        if (terms == 2)
+            hipLaunchKernelGGL((direct_gemm_kernel<true, 2>), dim3(cap), dim3(kDWaves * 64), 0, st, da);
+        else
+            hipLaunchKernelGGL((direct_gemm_kernel<true, 1>), dim3(cap), dim3(kDWaves * 64), 0, st, da);
+    }
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a1);
     if (mk) mk->mark(st);
@@ -2473,9 +2741,21 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         hipLaunchKernelGGL(large_m_gemm_kernel<false>, dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                            p.counts, p.offsets, s->n_experts);
     else if (direct)
-        hipLaunchKernelGGL(direct_gemm_kernel<false>, dim3(cap), dim3(kDWaves * 64), 0, st,
+        hipLaunchKernelGGL((direct_gemm_kernel<false, 0>), dim3(cap), dim3(kDWaves * 64), 0, st,
                            DArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
-                                 reinterpret_cast<const uint4 *>(w->packed + PL.s2), nullptr});
+                                 reinterpret_cast<const uint4 *>(w->packed + PL.s2), nullptr, nullptr});
+    else if (fp4) {
+        // rows past offsets[E] (the live rows) are skipped
+        launch_quantize_act(p.act, T * s->top_k, D, terms, p.offsets + s->n_experts, p.aq, p.aqs, st);
+        GemmArgs aq2 = a2;
+        aq2.A = reinterpret_cast<const uint16_t *>(p.aq);
+        const DArgs da{aq2, reinterpret_cast<const uint4 *>(w->packed_fp4 + PL.w2),
+                       reinterpret_cast<const uint4 *>(w->packed_fp4 + PL.s2), nullptr, p.aqs};
+        if (terms == 2)
+            hipLaunchKernelGGL((direct_gemm_kernel<false, 2>), dim3(cap), dim3(kDWaves * 64), 0, st, da);
+        else
+            hipLaunchKernelGGL((direct_gemm_kernel<false, 1>), dim3(cap), dim3(kDWaves * 64), 0, st, da);
+    }
     else
         hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(cap), dim3(kSmallWaves * 64), 0, st, a2);
     if (mk) mk->mark(st);
@@ -2556,7 +2836,7 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     const Ptrs p = ws_ptrs(L, workspace);
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
                       gemm_tile_rows(shape, w, n_tokens, flags),
-                      gemm_path(shape, w, n_tokens, flags) != PATH_DIRECT);
+                      gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT);
     if (rc) return rc;
     return launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream);
 }
@@ -2581,7 +2861,7 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
     mk.mark(stream);
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
                       gemm_tile_rows(shape, w, n_tokens, flags),
-                      gemm_path(shape, w, n_tokens, flags) != PATH_DIRECT, &mk);
+                      gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT, &mk);
     if (!rc) rc = launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream, &mk);
     if (!rc) rc = hip_status(hipEventSynchronize(mk.ev[5]));
     for (int i = 0; i < 5 && !rc; ++i)
@@ -2643,8 +2923,8 @@ size_t gptoss_moe_packed_size(const gptoss_moe_shape *shape) {
     return pack_layout(*shape).total;
 }
 
-int gptoss_moe_pack_weights(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
-                            void *packed, size_t bytes, hipStream_t stream) {
+static int pack_weights_fmt(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                            void *packed, size_t bytes, hipStream_t stream, int fmt) {
     if (!shape_ok(shape) || !w || !w->w1 || !w->w1_scales || !w->w2 || !w->w2_scales || !packed)
         return GPTOSS_MOE_ERR_INVALID_ARG;
     if (shape->hidden > kMaxHidden || shape->intermediate > kMaxHidden)
@@ -2657,9 +2937,28 @@ int gptoss_moe_pack_weights(const gptoss_moe_shape *shape, const gptoss_moe_weig
     const int H = shape->hidden, D = shape->intermediate, E = shape->n_experts;
     const int grid = 4 * device_cus();
     hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(256), 0, stream, w->w1, w->w1_scales, 2 * D, H,
-                       E, 1, reinterpret_cast<uint32_t *>(pb + L.w1), pb + L.s1);
+                       E, 1, fmt, reinterpret_cast<uint32_t *>(pb + L.w1), pb + L.s1);
     hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(256), 0, stream, w->w2, w->w2_scales, H, D, E,
-                       0, reinterpret_cast<uint32_t *>(pb + L.w2), pb + L.s2);
+                       0, fmt, reinterpret_cast<uint32_t *>(pb + L.w2), pb + L.s2);
+    return hip_status(hipGetLastError());
+}
+
+int gptoss_moe_pack_weights(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                            void *packed, size_t bytes, hipStream_t stream) {
+    return pack_weights_fmt(shape, w, packed, bytes, stream, 0);
+}
+
+int gptoss_moe_pack_weights_fp4(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                                void *packed, size_t bytes, hipStream_t stream) {
+    return pack_weights_fmt(shape, w, packed, bytes, stream, 1);
+}
+
+int gptoss_moe_quantize_act(const uint16_t *x, int rows, int k_cols, int terms, uint8_t *q,
+                            uint8_t *q_scales, hipStream_t stream) {
+    if (rows < 0 || k_cols <= 0 || k_cols % 8 || (terms != 1 && terms != 2)) return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (rows == 0) return GPTOSS_MOE_OK;
+    if (!x || !q || !q_scales || !aligned16(x) || ((uintptr_t)q & 7)) return GPTOSS_MOE_ERR_INVALID_ARG;
+    launch_quantize_act(x, rows, k_cols, terms, nullptr, q, q_scales, stream);
     return hip_status(hipGetLastError());
 }
 

@@ -28,7 +28,12 @@ ERR_UNSUPPORTED = -4
 FLAG_RESIDUAL_ADD = 1
 FLAG_SMALL_M_GEMM = 2
 FLAG_LARGE_M_GEMM = 4
-_PATH_FLAGS = {"auto": 0, "small": FLAG_SMALL_M_GEMM, "large": FLAG_LARGE_M_GEMM}
+FLAG_FP4_MFMA = 8
+FLAG_FP8_ACT = 16
+# "fp4": block-scaled FP4 MFMA on MXFP8 activations (hi + lo terms); "fp4_fp8":
+# the same with the hi term only.  Both need the packed_fp4 weights (pack_fp4()).
+_PATH_FLAGS = {"auto": 0, "small": FLAG_SMALL_M_GEMM, "large": FLAG_LARGE_M_GEMM,
+               "fp4": FLAG_FP4_MFMA, "fp4_fp8": FLAG_FP4_MFMA | FLAG_FP8_ACT}
 
 _ERRNAMES = {ERR_INVALID_ARG: "invalid argument", ERR_WORKSPACE: "workspace too small",
              ERR_HIP: "HIP error", ERR_UNSUPPORTED: "unsupported shape"}
@@ -50,7 +55,7 @@ class Shape(ctypes.Structure):
 class Weights(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
                 ("router_w", "router_b", "w1", "w1_scales", "b1", "w2", "w2_scales", "b2",
-                 "packed")]
+                 "packed", "packed_fp4")]
 
 
 class Views(ctypes.Structure):
@@ -86,6 +91,10 @@ _SIGS = {
     "gptoss_moe_packed_size": (ctypes.c_size_t, [ctypes.POINTER(Shape)]),
     "gptoss_moe_pack_weights": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights),
                                                _VP, ctypes.c_size_t, _VP]),
+    "gptoss_moe_pack_weights_fp4": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights),
+                                                   _VP, ctypes.c_size_t, _VP]),
+    "gptoss_moe_quantize_act": (ctypes.c_int, [_VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP,
+                                               _VP, _VP]),
     "gptoss_moe_last_hip_error": (ctypes.c_int, []),
     "gptoss_moe_version": (ctypes.c_char_p, []),
 }
@@ -140,7 +149,7 @@ class MoeLayer:
     """
 
     def __init__(self, shape: Shape, weights: dict, max_tokens: int, device="cuda",
-                 pack: bool = True):
+                 pack: bool = True, pack_fp4: bool = False):
         import torch
         self.lib = load_library()
         self.shape = shape
@@ -148,9 +157,12 @@ class MoeLayer:
         self.device = torch.device(device)
         self.tensors = dict(weights)  # keep device buffers alive
         self.tensors.pop("packed", None)
+        self.tensors.pop("packed_fp4", None)
         self.w = Weights(*[_ptr(self.tensors.get(n)) for n, _ in Weights._fields_])
         if pack:
             self.pack()
+        if pack_fp4:
+            self.pack_fp4()
         self.ws_bytes = workspace_size(shape, self.max_tokens)
         if self.ws_bytes == 0:
             raise MoeError("gptoss_moe_workspace_size", ERR_INVALID_ARG)
@@ -172,6 +184,21 @@ class MoeLayer:
         self.tensors["packed"] = buf
         self.w.packed = buf.data_ptr()
 
+    def pack_fp4(self):
+        """Build the scaled-MFMA-ordered copy (gptoss_moe_pack_weights_fp4) for
+        the "fp4" / "fp4_fp8" paths."""
+        import torch
+        n = int(self.lib.gptoss_moe_packed_size(ctypes.byref(self.shape)))
+        if n == 0:
+            raise MoeError("gptoss_moe_packed_size", ERR_INVALID_ARG)
+        buf = torch.empty(n, dtype=torch.uint8, device=self.device)
+        _check("gptoss_moe_pack_weights_fp4",
+               self.lib.gptoss_moe_pack_weights_fp4(ctypes.byref(self.shape),
+                                                    ctypes.byref(self.w), buf.data_ptr(), n,
+                                                    _stream()))
+        self.tensors["packed_fp4"] = buf
+        self.w.packed_fp4 = buf.data_ptr()
+
     def unpack(self):
         """Drop the packed copy: later calls read w1/w2 directly."""
         self.tensors.pop("packed", None)
@@ -179,7 +206,7 @@ class MoeLayer:
 
     @classmethod
     def from_numpy(cls, d, max_tokens: Optional[int] = None, device="cuda",
-                   pack: bool = True) -> "MoeLayer":
+                   pack: bool = True, pack_fp4: bool = False) -> "MoeLayer":
         """Upload a synth.MoeData layer."""
         import torch
         c = d.cfg
@@ -195,13 +222,14 @@ class MoeLayer:
              "w1_scales": up(d.s1), "b1": up(d.b1), "w2": up(d.w2), "w2_scales": up(d.s2),
              "b2": up(d.b2)}
         shape = make_shape(c.hidden, c.intermediate, c.n_experts, c.top_k)
-        return cls(shape, w, max_tokens or c.tokens, device, pack=pack)
+        return cls(shape, w, max_tokens or c.tokens, device, pack=pack, pack_fp4=pack_fp4)
 
     # -- entry points ---------------------------------------------------
     def forward(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,
                 stream=None, path="auto"):
         """e_agg (or out + e_agg with residual=True) for bf16 rows x_norm [T][H].
-        path: "auto", or "small" / "large" to force the grouped-GEMM path."""
+        path: "auto", "small" / "large" to force a grouped-GEMM path, or
+        "fp4" / "fp4_fp8" for the block-scaled FP4 MFMA variant."""
         import torch
         T = x_norm.shape[0]
         if out is None:
@@ -315,3 +343,21 @@ def quantize_mxfp4(src, stream=None):
                                                   _stream(stream))
     _check("gptoss_moe_quantize_mxfp4", rc)
     return packed, scales
+
+
+def quantize_act(x, terms: int = 2, stream=None):
+    """bf16 device rows [rows][K] -> MXFP8 codes uint8 [rows][ceil(K/512)*1024] and
+    scales uint8 [rows][ceil(K/512)*32] of the FP4-MFMA variant
+    (gptoss_moe_quantize_act)."""
+    import torch
+    if x.dtype not in (torch.int16, torch.uint16, torch.bfloat16) or x.dim() != 2:
+        raise TypeError("quantize_act takes bf16 bits [rows][K]")
+    x = x.contiguous()
+    rows, K = x.shape
+    KS = (K + 511) // 512
+    q = torch.empty((rows, KS * 1024), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, KS * 32), dtype=torch.uint8, device=x.device)
+    rc = load_library().gptoss_moe_quantize_act(_ptr(x), rows, K, terms, _ptr(q), _ptr(s),
+                                                _stream(stream))
+    _check("gptoss_moe_quantize_act", rc)
+    return q, s

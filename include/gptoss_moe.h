@@ -49,6 +49,17 @@ extern "C" {
  * >= 256 and falls back to small-M otherwise). */
 #define GPTOSS_MOE_FLAG_SMALL_M_GEMM 2u
 #define GPTOSS_MOE_FLAG_LARGE_M_GEMM 4u
+/* Block-scaled FP4 MFMA variant (no counterpart in the reference; an extra
+ * measured variant, never the default, because it quantises activations):
+ * the expert GEMMs run v_mfma_scale_f32_16x16x128_f8f6f4 on weights.packed_fp4
+ * (required) with the activations (x, then the SwiGLU output) quantised per
+ * 32-k group to MXFP8 e4m3 as two terms, hi + lo (a bf16 value is carried to
+ * within 2^-8 of its group's maximum, in practice exactly).  FP8_ACT keeps
+ * the hi term only (half the MFMA work, about 3% relative error per
+ * activation).  Weight e8m0 bytes 0 and 255 act as 2^-127 and NaN here (the
+ * reference: 0 and +Inf).  Not combinable with SMALL_M / LARGE_M. */
+#define GPTOSS_MOE_FLAG_FP4_MFMA 8u
+#define GPTOSS_MOE_FLAG_FP8_ACT 16u
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {
@@ -73,8 +84,10 @@ typedef struct gptoss_moe_weights {
     const uint16_t *b2;        /* bf16 [E][H] */
     const uint8_t *packed;     /* optional: w1/w2 and their scales rearranged by
                                 * gptoss_moe_pack_weights (NULL = not packed).
-                                * When set, small batches run the direct GEMM
-                                * on it; w1/w2 are still read by large ones. */
+                                * When set, the direct GEMM runs on it. */
+    const uint8_t *packed_fp4; /* optional: the same rearranged by
+                                * gptoss_moe_pack_weights_fp4 for
+                                * GPTOSS_MOE_FLAG_FP4_MFMA (NULL = absent). */
 } gptoss_moe_weights;
 
 /* Views into a workspace after a call, for inspection and parity tests.
@@ -196,6 +209,26 @@ int gptoss_moe_quantize_mxfp4(const float *src, int64_t n_elems, uint8_t *packed
 size_t gptoss_moe_packed_size(const gptoss_moe_shape *shape);
 int gptoss_moe_pack_weights(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
                             void *packed, size_t bytes, hipStream_t stream);
+/* The same packing in the operand order of the block-scaled FP4 MFMA
+ * (weights.packed_fp4, GPTOSS_MOE_FLAG_FP4_MFMA); no counterpart in the
+ * reference.  Same size (gptoss_moe_packed_size) and alignment. */
+int gptoss_moe_pack_weights_fp4(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                                void *packed, size_t bytes, hipStream_t stream);
+
+/*
+ * Activation quantiser of GPTOSS_MOE_FLAG_FP4_MFMA (no counterpart in the
+ * reference), exposed for tests and callers that quantise ahead: bf16 x
+ * [rows][k_cols] (k_cols a multiple of 8) -> MXFP8 e4m3 codes and e8m0 scales.
+ * Per 32-k group: e = floor(log2 max|x|) - 7 clamped to [-123, 120] (0 for
+ * an all-zero group); hi = e4m3_rne(x 2^-e); lo = e4m3_rne((x 2^-e - hi) 16)
+ * for terms = 2, else 0; scales e + 127 (hi), e + 123 (lo).  Per row,
+ * ceil(k_cols/512) stages: q gets 1 KB each (512 B hi, 512 B lo; byte
+ * 128 kp + 32 g + 16 h + j of a half is k = 512 s + 128 kp + 64 h + 16 g + j,
+ * 0 past k_cols), q_scales 32 B each (16 B hi, 16 B lo; byte 4 g + b is the
+ * 32-k group 16 s + 4 b + g).
+ */
+int gptoss_moe_quantize_act(const uint16_t *x, int rows, int k_cols, int terms, uint8_t *q,
+                            uint8_t *q_scales, hipStream_t stream);
 
 /* Last HIP error seen by this library on the calling thread (hipError_t). */
 int gptoss_moe_last_hip_error(void);

@@ -295,6 +295,113 @@ int orc_route_index(const int32_t *ti, const uint16_t *tw, int T, int K, int E, 
     return dropped;
 }
 
+/* ------------------------------------------- MXFP8 activations (variant) -- */
+/*
+ * Activation quantiser of the block-scaled FP4 MFMA variant (no counterpart in
+ * the reference, whose GEMMs take bf16 activations; the variant's own rule):
+ * per 32-element block along K, e = floor(log2 max|x|) - 7 clamped to
+ * [-123, 120] (0 for an all-zero block); hi = e4m3_rne(x * 2^-e), and for two
+ * terms lo = e4m3_rne((x * 2^-e - hi) * 16); e8m0 scales e + 127 (hi) and
+ * e + 123 (lo).  x = hi * 2^e + lo * 2^(e-4) up to the rounding of lo.
+ * Layout per row: ceil(K/512) stages of 1 KB (512 B hi, then 512 B lo); in a
+ * stage, k step kp (128 k) is 128 bytes whose byte 32 g + 16 h + j is
+ * k = 128 kp + 64 h + 16 g + j (the MFMA's A-operand order: lane group g
+ * holds k 16 g .. + 15 and 64 + 16 g .. + 15).  Scales per row and stage:
+ * 16 B hi then 16 B lo; byte 4 g + b is 32-k group 4 b + g.  k >= K: code 0.
+ */
+
+/* OCP e4m3 (bias 7, no infinities) of a finite v with |v| < 464, round to
+ * nearest even; the sign is kept (a negative value rounding to 0 is 0x80). */
+static uint8_t orc_e4m3_rne(float v) {
+    const uint8_t sgn = signbit(v) ? 0x80 : 0;
+    const float a = fabsf(v);
+    if (a < 0x1p-6f) return sgn | (uint8_t)(int)rintf(a * 512.0f); /* multiples of 2^-9; 8 = 2^-6 */
+    int E;
+    frexpf(a, &E);
+    E -= 1; /* a in [2^E, 2^(E+1)) */
+    int q = (int)rintf(ldexpf(a, 3 - E)); /* 8 .. 16 */
+    if (q == 16) {
+        q = 8;
+        E += 1;
+    }
+    return sgn | (uint8_t)(((E + 7) << 3) | (q - 8));
+}
+
+float orc_e4m3_dec(uint8_t c) {
+    const int e = (c >> 3) & 15, m = c & 7;
+    const float v = e == 0 ? ldexpf((float)m, -9) : ldexpf((float)(8 + m), e - 10);
+    return (c & 0x80) ? -v : v;
+}
+
+static int64_t orc_aq_pos(int k) {
+    const int j = k / 512, kk = k % 512, kp = kk / 128, kin = kk % 128;
+    const int g = (kin % 64) / 16, h = kin / 64, jj = kin % 16;
+    return (int64_t)j * 1024 + kp * 128 + 32 * g + 16 * h + jj;
+}
+static int64_t orc_aq_spos(int b) { /* 32-k group b -> scale byte of its row */
+    const int j = b / 16, bs = b % 16;
+    return (int64_t)j * 32 + 4 * (bs % 4) + bs / 4;
+}
+
+void orc_quantize_act(const uint16_t *x, int rows, int K, int terms, uint8_t *q, uint8_t *s) {
+    const int KS = (K + 511) / 512;
+    memset(q, 0, (size_t)rows * KS * 1024);
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *xr = x + (int64_t)r * K;
+        uint8_t *qr = q + (int64_t)r * KS * 1024, *sr = s + (int64_t)r * KS * 32;
+        for (int b = 0; b < KS * 16; ++b) {
+            float amax = 0.0f;
+            for (int k = 32 * b; k < 32 * b + 32 && k < K; ++k) amax = fmaxf(amax, fabsf(orc_bf2f(xr[k])));
+            int e = 0;
+            if (amax > 0.0f) {
+                int E;
+                frexpf(amax, &E);
+                e = E - 1 - 7;
+                e = e < -123 ? -123 : (e > 120 ? 120 : e);
+            }
+            sr[orc_aq_spos(b)] = (uint8_t)(e + 127);
+            sr[orc_aq_spos(b) + 16] = (uint8_t)(e + 123);
+            for (int k = 32 * b; k < 32 * b + 32 && k < K; ++k) {
+                const float v = ldexpf(orc_bf2f(xr[k]), -e);
+                const uint8_t hi = orc_e4m3_rne(v);
+                qr[orc_aq_pos(k)] = hi;
+                qr[orc_aq_pos(k) + 512] = terms == 2 ? orc_e4m3_rne((v - orc_e4m3_dec(hi)) * 16.0f) : 0;
+            }
+        }
+    }
+}
+
+/* The values the variant's GEMM sees: hi * 2^(sh-127) + lo * 2^(sl-127). */
+void orc_dequant_act(const uint8_t *q, const uint8_t *s, int rows, int K, float *out) {
+    const int KS = (K + 511) / 512;
+    for (int r = 0; r < rows; ++r) {
+        const uint8_t *qr = q + (int64_t)r * KS * 1024, *sr = s + (int64_t)r * KS * 32;
+        for (int k = 0; k < K; ++k) {
+            const int64_t sp = orc_aq_spos(k / 32);
+            const double v = (double)orc_e4m3_dec(qr[orc_aq_pos(k)]) * ldexp(1.0, sr[sp] - 127) +
+                             (double)orc_e4m3_dec(qr[orc_aq_pos(k) + 512]) * ldexp(1.0, sr[sp + 16] - 127);
+            out[(int64_t)r * K + k] = (float)v;
+        }
+    }
+}
+
+/* Rows of bf16 x [rows][K] replaced in place (as float) by what the variant's
+ * GEMM sees for activation mode aq (0 = bf16 as is, 1 = one MXFP8 term,
+ * 2 = two). */
+static void orc_act_as_seen(const uint16_t *x, int rows, int K, int aq, float *out) {
+    if (aq == 0) {
+        for (int64_t i = 0; i < (int64_t)rows * K; ++i) out[i] = orc_bf2f(x[i]);
+        return;
+    }
+    const int KS = (K + 511) / 512;
+    uint8_t *q = (uint8_t *)malloc((size_t)rows * KS * 1024 + 1);
+    uint8_t *s = (uint8_t *)malloc((size_t)rows * KS * 32 + 1);
+    orc_quantize_act(x, rows, K, aq, q, s);
+    orc_dequant_act(q, s, rows, K, out);
+    free(q);
+    free(s);
+}
+
 /* ------------------------------------------------------------ experts -- */
 
 static double orc_dot(const float *a, const float *b, int n) {
@@ -326,10 +433,11 @@ static float orc_swiglu(float g, float u, float limit, float alpha) {
  * b2) (TP = 1, getp_run.cpp:951-967); reduction (moe.hpp:700-730): fmaf over
  * the k slots in slot order, fp32, then bf16.
  */
-void orc_moe_experts(int H, int D, int E, int K, float limit, float alpha, const uint16_t *x_norm,
-                     const uint8_t *w1, const uint8_t *s1, const uint16_t *b1, const uint8_t *w2,
-                     const uint8_t *s2, const uint16_t *b2, const int32_t *ti, const uint16_t *tw,
-                     int T, uint16_t *e_agg, uint16_t *act_out) {
+static void orc_moe_experts_aq(int H, int D, int E, int K, float limit, float alpha,
+                               const uint16_t *x_norm, const uint8_t *w1, const uint8_t *s1,
+                               const uint16_t *b1, const uint8_t *w2, const uint8_t *s2,
+                               const uint16_t *b2, const int32_t *ti, const uint16_t *tw, int T,
+                               uint16_t *e_agg, uint16_t *act_out, int aq) {
     const int N1 = 2 * D;
     int32_t *counts = (int32_t *)malloc(sizeof(int32_t) * E);
     int32_t *offsets = (int32_t *)malloc(sizeof(int32_t) * (E + 1));
@@ -340,8 +448,8 @@ void orc_moe_experts(int H, int D, int E, int K, float limit, float alpha, const
     const int P = offsets[E];
     uint16_t *y = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)P * H + 2);
     uint16_t *act = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)P * D + 2);
-    float *xf = (float *)malloc(sizeof(float) * (size_t)T * H);
-    for (int64_t i = 0; i < (int64_t)T * H; ++i) xf[i] = orc_bf2f(x_norm[i]);
+    float *xf = (float *)malloc(sizeof(float) * (size_t)T * H + 4);
+    orc_act_as_seen(x_norm, T, H, aq, xf);
     float *W = (float *)malloc(sizeof(float) * (size_t)N1 * H);
     float *hrow = (float *)malloc(sizeof(float) * (size_t)(P > 0 ? P : 1) * D);
     for (int e = 0; e < E; ++e) {
@@ -360,9 +468,9 @@ void orc_moe_experts(int H, int D, int E, int K, float limit, float alpha, const
                 u = orc_bf2f(orc_f2bf(u + orc_bf2f(b1[(int64_t)e * N1 + 2 * j + 1])));
                 uint16_t a = orc_f2bf(orc_swiglu(g, u, limit, alpha));
                 act[(int64_t)(r0 + r) * D + j] = a;
-                hrow[(int64_t)r * D + j] = orc_bf2f(a);
             }
         }
+        orc_act_as_seen(act + (int64_t)r0 * D, nr, D, aq, hrow);
         /* MLP2 */
         const int64_t seg2 = (int64_t)H * D;
         orc_dequant_mxfp4_f32(w2 + e * (seg2 / 2), s2 + e * (seg2 / 32), seg2, W);
@@ -386,6 +494,14 @@ void orc_moe_experts(int H, int D, int E, int K, float limit, float alpha, const
     if (act_out) memcpy(act_out, act, sizeof(uint16_t) * (size_t)P * D);
     free(counts); free(offsets); free(local_ids); free(row_token); free(row_w);
     free(y); free(act); free(xf); free(W); free(hrow);
+}
+
+void orc_moe_experts(int H, int D, int E, int K, float limit, float alpha, const uint16_t *x_norm,
+                     const uint8_t *w1, const uint8_t *s1, const uint16_t *b1, const uint8_t *w2,
+                     const uint8_t *s2, const uint16_t *b2, const int32_t *ti, const uint16_t *tw,
+                     int T, uint16_t *e_agg, uint16_t *act_out) {
+    orc_moe_experts_aq(H, D, E, K, limit, alpha, x_norm, w1, s1, b1, w2, s2, b2, ti, tw, T, e_agg,
+                       act_out, 0);
 }
 
 /* ----------------------------------------------------- layer boundary -- */
@@ -423,11 +539,13 @@ void orc_residual_add(uint16_t *x, const uint16_t *e, int64_t n) {
 
 /* Whole MoE on normalised rows, getp semantics: router (or forced routing
  * when ti_in != NULL), experts, reduction.  Optional outputs may be NULL. */
-void orc_moe_forward(int H, int D, int E, int K, float limit, float alpha, const uint16_t *x_norm,
-                     const uint16_t *wr, const uint16_t *br, const uint8_t *w1, const uint8_t *s1,
-                     const uint16_t *b1, const uint8_t *w2, const uint8_t *s2, const uint16_t *b2,
-                     int T, const int32_t *ti_in, const uint16_t *tw_in, uint16_t *e_agg,
-                     uint16_t *logits_out, int32_t *ti_out, uint16_t *tw_out) {
+/* aq: activations as the FP4-MFMA variant sees them (0 = bf16 path). */
+void orc_moe_forward_aq(int H, int D, int E, int K, float limit, float alpha,
+                        const uint16_t *x_norm, const uint16_t *wr, const uint16_t *br,
+                        const uint8_t *w1, const uint8_t *s1, const uint16_t *b1,
+                        const uint8_t *w2, const uint8_t *s2, const uint16_t *b2, int T,
+                        const int32_t *ti_in, const uint16_t *tw_in, uint16_t *e_agg,
+                        uint16_t *logits_out, int32_t *ti_out, uint16_t *tw_out, int aq) {
     int32_t *ti = (int32_t *)malloc(sizeof(int32_t) * (size_t)T * K + 4);
     uint16_t *tw = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * K + 4);
     if (ti_in) {
@@ -440,12 +558,21 @@ void orc_moe_forward(int H, int D, int E, int K, float limit, float alpha, const
         if (logits_out) memcpy(logits_out, lg, sizeof(uint16_t) * (size_t)T * E);
         free(lg);
     }
-    orc_moe_experts(H, D, E, K, limit, alpha, x_norm, w1, s1, b1, w2, s2, b2, ti, tw, T, e_agg,
-                    NULL);
+    orc_moe_experts_aq(H, D, E, K, limit, alpha, x_norm, w1, s1, b1, w2, s2, b2, ti, tw, T, e_agg,
+                       NULL, aq);
     if (ti_out) memcpy(ti_out, ti, sizeof(int32_t) * (size_t)T * K);
     if (tw_out) memcpy(tw_out, tw, sizeof(uint16_t) * (size_t)T * K);
     free(ti);
     free(tw);
+}
+
+void orc_moe_forward(int H, int D, int E, int K, float limit, float alpha, const uint16_t *x_norm,
+                     const uint16_t *wr, const uint16_t *br, const uint8_t *w1, const uint8_t *s1,
+                     const uint16_t *b1, const uint8_t *w2, const uint8_t *s2, const uint16_t *b2,
+                     int T, const int32_t *ti_in, const uint16_t *tw_in, uint16_t *e_agg,
+                     uint16_t *logits_out, int32_t *ti_out, uint16_t *tw_out) {
+    orc_moe_forward_aq(H, D, E, K, limit, alpha, x_norm, wr, br, w1, s1, b1, w2, s2, b2, T, ti_in,
+                       tw_in, e_agg, logits_out, ti_out, tw_out, 0);
 }
 
 /* ------------------------------------------------- fp32 CPU engine ----- */

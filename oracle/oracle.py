@@ -35,6 +35,11 @@ _SIGS = {
     "orc_residual_add": (None, [_P, _P, _I64]),
     "orc_moe_forward": (None, [_I, _I, _I, _I, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                                _P, _P, _P, _P, _P, _P]),
+    "orc_moe_forward_aq": (None, [_I, _I, _I, _I, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                                  _P, _P, _P, _P, _P, _P, _I]),
+    "orc_quantize_act": (None, [_P, _I, _I, _I, _P, _P]),
+    "orc_dequant_act": (None, [_P, _P, _I, _I, _P]),
+    "orc_e4m3_dec": (_F, [ctypes.c_uint8]),
     "orc_moe_fp32_token": (None, [_I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "orc_num_threads": (_I, []),
 }
@@ -92,6 +97,30 @@ def quantize_mxfp4(src):
     return packed, scales
 
 
+def quantize_act(x, terms: int):
+    """bf16 [rows][K] -> MXFP8 activations of the FP4-MFMA variant:
+    (q uint8 [rows][ceil(K/512)*1024], s uint8 [rows][ceil(K/512)*32])."""
+    x = _c(x, np.uint16)
+    rows, K = x.shape
+    KS = (K + 511) // 512
+    q = np.empty((rows, KS * 1024), np.uint8)
+    s = np.empty((rows, KS * 32), np.uint8)
+    lib().orc_quantize_act(_p(x), rows, K, terms, _p(q), _p(s))
+    return q, s
+
+
+def dequant_act(q, s, K: int) -> np.ndarray:
+    q, s = _c(q, np.uint8), _c(s, np.uint8)
+    rows = q.shape[0]
+    out = np.empty((rows, K), np.float32)
+    lib().orc_dequant_act(_p(q), _p(s), rows, K, _p(out))
+    return out
+
+
+def e4m3_decode_table() -> np.ndarray:
+    return np.array([lib().orc_e4m3_dec(c) for c in range(256)], np.float32)
+
+
 def router_logits(x, wr) -> np.ndarray:
     x, wr = _c(x, np.uint16), _c(wr, np.uint16)
     T, H = x.shape
@@ -138,10 +167,12 @@ def moe_experts(d, x_norm, ti, tw, want_act=False):
     return (out, act) if want_act else out
 
 
-def moe_forward(d, x_norm=None, forced=True, rows=None):
+def moe_forward(d, x_norm=None, forced=True, rows=None, act_quant=0):
     """getp-semantics MoE of a synth.MoeData layer.  Returns dict with
     e_agg, logits (router runs only), topk_i, topk_w.  `rows` selects a
-    subset of tokens (each token's result depends on that token only)."""
+    subset of tokens (each token's result depends on that token only).
+    act_quant 1 / 2: the expert GEMMs see their activations as the FP4-MFMA
+    variant quantises them (one / two MXFP8 terms)."""
     c = d.cfg
     x = d.x if x_norm is None else x_norm
     fi, fw = (d.forced_i, d.forced_w) if forced else (None, None)
@@ -158,9 +189,10 @@ def moe_forward(d, x_norm=None, forced=True, rows=None):
     tw = np.empty((T, K), np.uint16)
     if fi is not None:
         fi, fw = _c(fi, np.int32), _c(fw, np.uint16)
-    lib().orc_moe_forward(c.hidden, c.intermediate, E, K, 7.0, 1.702, _p(x), _p(d.router_w),
-                          _p(d.router_b), _p(d.w1), _p(d.s1), _p(d.b1), _p(d.w2), _p(d.s2),
-                          _p(d.b2), T, _p(fi), _p(fw), _p(e_agg), _p(lg), _p(ti), _p(tw))
+    lib().orc_moe_forward_aq(c.hidden, c.intermediate, E, K, 7.0, 1.702, _p(x), _p(d.router_w),
+                             _p(d.router_b), _p(d.w1), _p(d.s1), _p(d.b1), _p(d.w2), _p(d.s2),
+                             _p(d.b2), T, _p(fi), _p(fw), _p(e_agg), _p(lg), _p(ti), _p(tw),
+                             act_quant)
     return {"e_agg": e_agg, "logits": lg if fi is None else None, "topk_i": ti, "topk_w": tw}
 
 

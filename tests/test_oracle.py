@@ -332,3 +332,110 @@ def test_quantize_round_trip_exact():
     assert np.array_equal(s2, sc)
     want = np.where(codes.reshape(-1) == 8, 0, codes.reshape(-1))
     assert np.array_equal(_unpack(p2, nb * 32), want)
+
+
+# ------------------------------------------ MXFP8 activations (FP4 variant) --
+# OCP FP8 e4m3 known answers (bias 7, no infinities, 0x7f NaN): 0x38 = 1.0,
+# 0x7e = 448 (largest), 0x08 = 2^-6 (smallest normal), 0x01 = 2^-9.
+def test_e4m3_known_values():
+    t = oracle.e4m3_decode_table()
+    assert t[0x38] == 1.0 and t[0x7E] == 448.0 and t[0x08] == 2.0 ** -6 and t[0x01] == 2.0 ** -9
+    assert t[0xB8] == -1.0 and t[0x00] == 0.0 and np.signbit(t[0x80])
+    pos = t[:0x7F]
+    assert np.all(np.diff(pos) > 0)  # codes 0..126 ascend
+
+
+def _e4m3_nearest_even(v):
+    """Brute force: the nearest of the 127 non-negative e4m3 values, ties to
+    the even code (last mantissa bit 0), sign applied after."""
+    t = oracle.e4m3_decode_table()[:0x7F].astype(np.float64)
+    a = np.abs(v.astype(np.float64))[:, None]
+    d = np.abs(t[None, :] - a)
+    best = d.min(axis=1, keepdims=True)
+    cand = d == best
+    code = np.where(cand.sum(1) > 1, np.argmax(cand & (np.arange(127) % 2 == 0)[None, :], 1),
+                    np.argmax(cand, 1)).astype(np.uint8)
+    return code | np.where(np.signbit(v), 0x80, 0).astype(np.uint8)
+
+
+def _qa_pos(k):
+    """Byte of k within a row: 1 KB per 512-k stage, the MFMA A-operand order."""
+    j, kk = k // 512, k % 512
+    kp, kin = kk // 128, kk % 128
+    return j * 1024 + kp * 128 + 32 * ((kin % 64) // 16) + 16 * (kin // 64) + kin % 16
+
+
+def test_quantize_act_rounding_brute_force():
+    """Groups whose max is in [128, 256) have e = 0, so hi codes are e4m3_rne(x)
+    itself: checked against the brute-force nearest-even code, including every
+    tie between neighbouring codes."""
+    rng = np.random.default_rng(3)
+    t = oracle.e4m3_decode_table()[:0x7E].astype(np.float64)
+    mids = (t[:-1] + t[1:]) / 2
+    vals = np.concatenate([mids, rng.uniform(-250, 250, 4000), rng.uniform(-0.02, 0.02, 1000)])
+    vals = bf16_to_f32(f32_to_bf16(vals.astype(np.float32)))
+    vals = vals[np.abs(vals) < 255]
+    n = vals.size // 31 * 31
+    blocks = vals[:n].reshape(-1, 31)
+    x = np.concatenate([np.full((blocks.shape[0], 1), 255.0, np.float32), blocks], 1).reshape(1, -1)
+    K = x.shape[1] // 64 * 64
+    x = f32_to_bf16(x[:, :K])
+    q, s = oracle.quantize_act(x, 1)
+    xf = bf16_to_f32(x)[0]
+    got = q[0, _qa_pos(np.arange(K))]
+    assert np.array_equal(got, _e4m3_nearest_even(xf))
+    assert np.all(s[0, :] [np.arange(0, s.shape[1], 32)] == 127)
+
+
+def test_quantize_act_scale_rule_and_layout():
+    """Scale e = floor(log2 max|x|) - 7 (hi byte e + 127, lo e + 123), 0 for
+    an all-zero group, clamped at -123; group b's byte sits at 4 (b % 4) +
+    (b % 16) // 4 of its stage; codes follow the stated byte order."""
+    K = 1024
+    amax = [1.0, 3.0, 0.0, 2.0 ** -130, 1000.0, 2.0 ** 100] + [0.5] * 26
+    x = np.zeros((1, K), np.float32)
+    for b, a in enumerate(amax):
+        x[0, 32 * b + (b % 32)] = a
+    x = f32_to_bf16(x)
+    q, s = oracle.quantize_act(x, 2)
+    for b, a in enumerate(amax):
+        if a == 0.0:
+            e = 0
+        else:
+            e = max(int(np.floor(np.log2(float(bf16_to_f32(f32_to_bf16(np.float32(a))))))) - 7, -123)
+        j, bs = b // 16, b % 16
+        at = j * 32 + 4 * (bs % 4) + bs // 4
+        assert s[0, at] == e + 127 and s[0, at + 16] == e + 123, (b, a)
+    # the only nonzero hi code of group b is at k = 32 b + b % 32
+    hi = q[0].reshape(-1, 2, 512)[:, 0, :].reshape(-1)
+    nz = [int(i // 512) * 1024 + int(i % 512) for i in np.nonzero(hi)[0]]
+    want = sorted(_qa_pos(32 * b + (b % 32)) for b, a in enumerate(amax) if a != 0.0)
+    assert sorted(nz) == want
+
+
+def test_quantize_act_two_terms_error_bound():
+    """hi + lo reproduces x to within 2^-9 of its group's max scale 2^(e+7)
+    (the rounding of lo), and exactly when x has at most 7 significant bits."""
+    rng = np.random.default_rng(4)
+    v = rng.standard_normal((8, 2880)) * np.exp2(rng.integers(-20, 21, (8, 1)) + rng.standard_normal((8, 2880)) * 2)
+    x = f32_to_bf16(v.astype(np.float32))
+    q, s = oracle.quantize_act(x, 2)
+    y = oracle.dequant_act(q, s, 2880).astype(np.float64)
+    xf = bf16_to_f32(x).astype(np.float64)
+    g = np.abs(xf).reshape(8, -1, 32).max(2)
+    lim = np.repeat(np.exp2(np.floor(np.log2(np.maximum(g, 1e-300)))), 32, axis=1) * 2.0 ** -9
+    assert np.all(np.abs(y - xf) <= lim)
+    x7 = f32_to_bf16((np.round(rng.uniform(-127, 127, (4, 512))) * 2.0 ** -3).astype(np.float32))
+    q7, s7 = oracle.quantize_act(x7, 2)
+    assert np.array_equal(oracle.dequant_act(q7, s7, 512), bf16_to_f32(x7))
+
+
+def test_moe_forward_act_quant_two_terms_close_to_bf16():
+    """The variant's expected output with two terms stays within the layer
+    tolerance of the bf16 path's (the oracle, not the GPU)."""
+    from parity import compare
+    d = synth.make_data("c0_tiny")
+    a = oracle.moe_forward(d, forced=False)["e_agg"]
+    b = oracle.moe_forward(d, forced=False, act_quant=2)["e_agg"]
+    m = compare(b, a)
+    assert m["rel_l2"] < 1e-3, m
