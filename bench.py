@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--traffic", default="",
                     help="HBM traffic summary (default profiles/hbm_traffic_<config>.txt)")
@@ -99,6 +101,44 @@ def cpu_baseline(d, budget_s: float) -> dict:
     return {"value": n / dt, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
             "sample": f"{n} of {d.cfg.tokens} tokens of {d.cfg.name}, one token at a time "
                       f"(run.cpp:657-748 restated, fp32 weights = exact MXFP4 dequant), {dt:.1f} s"}
+
+
+def time_variants(layers, x, out, fi, fw, args, c, flops):
+    """Extra measured variants (never the headline): the block-scaled FP4 MFMA
+    path with MXFP8 activations, two terms (within the layer tolerance of the
+    bf16 oracle) and one term.  Same workload, same weight rotation, the
+    scaled-MFMA packing built once per copy outside the timed region."""
+    import statistics
+    import torch
+    for L in layers:
+        L.pack_fp4()
+    out_v = {}
+    for path, note in (("fp4", "MXFP8 activations, hi + lo terms"),
+                       ("fp4_fp8", "MXFP8 activations, hi term only")):
+        for i in range(args.warmup):
+            layers[i % len(layers)].forward(x, out, fi, fw, path=path)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            layers[i % len(layers)].forward(x, out, fi, fw, path=path)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        prof = {k: [] for k in layers[0].KERNELS}
+        for i in range(min(args.profile_iters, 10)):
+            r = layers[i % len(layers)].forward_profiled(x, out, fi, fw, path=path)
+            for k, v in r.items():
+                prof[k].append(v)
+        out_v[path] = {"flag": "GPTOSS_MOE_FLAG_FP4_MFMA" + (" | GPTOSS_MOE_FLAG_FP8_ACT" if path == "fp4_fp8" else ""),
+                       "activations": note, "ms_per_step": round(ms, 5),
+                       "tokens_per_s": round(c.tokens / (ms * 1e-3), 1),
+                       "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                       "kernel_ms": {k: round(statistics.median(v), 5) for k, v in prof.items()}}
+    for L in layers:
+        L.tensors.pop("packed_fp4", None)
+        L.w.packed_fp4 = None
+    return out_v
 
 
 def main():
@@ -168,6 +208,21 @@ def main():
         2 * pairs * D
     mlp1_gbs = mlp1_bytes / (kms["mlp1"] * 1e-3) / 1e9
     tok_s = c.tokens / (ms * 1e-3)
+    if c.tokens * c.top_k >= 96 * c.n_experts:
+        # prefill-sized: MLP1 is bound by the bf16 MFMA peak (2 D x H MACs per routed pair)
+        mlp1_flops = 2 * pairs * (2 * D) * H
+        tf = mlp1_flops / (kms["mlp1"] * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "kernel": "direct_gemm_kernel<true> (MLP1)",
+                    "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                    "algorithmic_flops_per_launch": mlp1_flops,
+                    "avg_launch_ms": round(kms["mlp1"], 5)}
+    else:
+        roofline = {"bound": "hbm", "kernel": "direct_gemm_kernel<true> (MLP1)",
+                    "achieved": round(mlp1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "algorithmic_bytes_per_launch": mlp1_bytes,
+                    "avg_launch_ms": round(kms["mlp1"], 5)}
     traffic = read_traffic(args.traffic or os.path.join(ROOT, "profiles", f"hbm_traffic_{c.name}.txt"),
                            "mlp1")
     res = {
@@ -188,11 +243,7 @@ def main():
         "config": {"workload": c.name, "hidden": H, "intermediate": D, "n_experts": c.n_experts,
                    "top_k": c.top_k, "tokens": c.tokens, "routing": c.routing,
                    "weight_copies_rotated": copies},
-        "roofline": {"bound": "hbm", "kernel": "direct_gemm_kernel<true> (MLP1)",
-                     "achieved": round(mlp1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": mlp1_bytes,
-                     "avg_launch_ms": round(kms["mlp1"], 5)},
+        "roofline": roofline,
         "layer": {"algorithmic_bytes": alg_bytes, "hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
                   "hbm_frac": round(alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                   "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
@@ -201,6 +252,8 @@ def main():
         "kernel_ms": {k: round(v, 5) for k, v in kms.items()},
         "wall_s_timed": round(wall, 4),
     }
+    if not args.no_variants:
+        res["variants"] = time_variants(layers, x, out, fi, fw, args, c, flops)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
     else:

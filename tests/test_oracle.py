@@ -402,7 +402,8 @@ def test_quantize_act_scale_rule_and_layout():
         if a == 0.0:
             e = 0
         else:
-            e = max(int(np.floor(np.log2(float(bf16_to_f32(f32_to_bf16(np.float32(a))))))) - 7, -123)
+            ab = float(bf16_to_f32(f32_to_bf16(np.array([a], np.float32)))[0])
+            e = max(int(np.floor(np.log2(ab))) - 7, -123)
         j, bs = b // 16, b % 16
         at = j * 32 + 4 * (bs % 4) + bs // 4
         assert s[0, at] == e + 127 and s[0, at + 16] == e + 123, (b, a)
