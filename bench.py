@@ -208,6 +208,8 @@ def main():
         2 * pairs * D
     mlp1_gbs = mlp1_bytes / (kms["mlp1"] * 1e-3) / 1e9
     tok_s = c.tokens / (ms * 1e-3)
+    traffic = read_traffic(args.traffic or os.path.join(ROOT, "profiles", f"hbm_traffic_{c.name}.txt"),
+                           "mlp1")
     if c.tokens * c.top_k >= 96 * c.n_experts:
         # prefill-sized: MLP1 is bound by the bf16 MFMA peak (2 D x H MACs per routed pair)
         mlp1_flops = 2 * pairs * (2 * D) * H
@@ -223,8 +225,6 @@ def main():
                     "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                     "algorithmic_bytes_per_launch": mlp1_bytes,
                     "avg_launch_ms": round(kms["mlp1"], 5)}
-    traffic = read_traffic(args.traffic or os.path.join(ROOT, "profiles", f"hbm_traffic_{c.name}.txt"),
-                           "mlp1")
     res = {
         "metric": METRIC,
         "value": round(tok_s, 1),
