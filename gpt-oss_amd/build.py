@@ -16,7 +16,7 @@ HIP_FLAGS = [
     "-I", os.path.join(ROOT, "include"),
 ]
 
-SOURCES = [os.path.join(HERE, "csrc", "gptoss_moe.hip")]
+SOURCES = [os.path.join(HERE, "csrc", "gptoss_moe.hip"), os.path.join(HERE, "csrc", "bin_loader.cpp")]
 LIB = os.path.join(HERE, "libgptoss_moe.so")
 
 

@@ -64,8 +64,36 @@ class Views(ctypes.Structure):
                  "row_weight", "row_slot", "act", "slots", "status")]
 
 
+class BinConfig(ctypes.Structure):
+    """The reference checkpoint's Config header (run.cpp:25-45)."""
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("vocab_size", "hidden_dim", "n_experts", "experts_per_token", "intermediate_dim",
+                 "n_layers", "head_dim", "n_attn_heads", "n_kv_heads", "seq_len",
+                 "initial_context_length")] + [
+        ("rope_theta", ctypes.c_float), ("rope_scaling_factor", ctypes.c_float),
+        ("sliding_window", ctypes.c_int), ("swiglu_limit", ctypes.c_float)]
+
+
+class BinLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in
+                ("rms_ffn_w", "w_router", "b_router", "w_mlp1", "b_mlp1", "w_mlp2", "b_mlp2",
+                 "file_bytes")]
+
+
+class BinDest(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("w1", "w1_scales", "b1", "w2", "w2_scales", "b2", "router_w", "router_b",
+                 "rms_ffn_w")]
+
+
 _VP = ctypes.c_void_p
 _SIGS = {
+    "gptoss_moe_bin_read_config": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(BinConfig)]),
+    "gptoss_moe_bin_layer_offsets": (ctypes.c_int, [ctypes.POINTER(BinConfig), ctypes.c_int,
+                                                    ctypes.POINTER(BinLayer)]),
+    "gptoss_moe_load_bin_layer": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int,
+                                                 ctypes.POINTER(BinDest), _VP, _VP,
+                                                 ctypes.c_size_t, _VP]),
     "gptoss_moe_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Shape), ctypes.c_int]),
     "gptoss_moe_workspace_init": (ctypes.c_int, [_VP, ctypes.c_size_t, _VP]),
     "gptoss_moe_workspace_views": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.c_int, _VP,
@@ -224,6 +252,37 @@ class MoeLayer:
         shape = make_shape(c.hidden, c.intermediate, c.n_experts, c.top_k)
         return cls(shape, w, max_tokens or c.tokens, device, pack=pack, pack_fp4=pack_fp4)
 
+    @classmethod
+    def from_bin(cls, path: str, layer: int, max_tokens: int, device="cuda", pack: bool = True,
+                 stage_bytes: int = 64 << 20) -> "MoeLayer":
+        """Layer `layer` of the reference's fp32 checkpoint (gptoss_moe_load_bin_layer):
+        MXFP4 quantised on the GPU, router / biases / RMSNorm weight in bf16 (kept
+        in tensors["rms_ffn_w"])."""
+        import torch
+        lib = load_library()
+        cfg = read_bin_config(path)
+        dev = torch.device(device)
+        H, D, E = cfg.hidden_dim, cfg.intermediate_dim, cfg.n_experts
+        u8 = lambda n: torch.empty(n, dtype=torch.uint8, device=dev)
+        i16 = lambda n: torch.empty(n, dtype=torch.int16, device=dev)
+        w = {"w1": u8(E * 2 * D * H // 2), "w1_scales": u8(E * 2 * D * H // 32),
+             "b1": i16(E * 2 * D), "w2": u8(E * H * D // 2), "w2_scales": u8(E * H * D // 32),
+             "b2": i16(E * H), "router_w": i16(E * H), "router_b": i16(E)}
+        rms = i16(H)
+        dst = BinDest(*[_ptr(w[n]) for n in ("w1", "w1_scales", "b1", "w2", "w2_scales", "b2",
+                                                "router_w", "router_b")], _ptr(rms))
+        stage_h = torch.empty(stage_bytes, dtype=torch.uint8, pin_memory=True)
+        stage_d = u8(stage_bytes)
+        rc = lib.gptoss_moe_load_bin_layer(path.encode(), layer, ctypes.byref(dst),
+                                           stage_h.data_ptr(), stage_d.data_ptr(), stage_bytes,
+                                           _stream())
+        _check("gptoss_moe_load_bin_layer", rc)
+        torch.cuda.synchronize(dev)
+        shape = make_shape(H, D, E, cfg.experts_per_token, cfg.swiglu_limit)
+        layer_obj = cls(shape, w, max_tokens, device, pack=pack)
+        layer_obj.tensors["rms_ffn_w"] = rms
+        return layer_obj
+
     # -- entry points ---------------------------------------------------
     def forward(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,
                 stream=None, path="auto"):
@@ -361,3 +420,17 @@ def quantize_act(x, terms: int = 2, stream=None):
                                                 _stream(stream))
     _check("gptoss_moe_quantize_act", rc)
     return q, s
+
+
+def read_bin_config(path: str) -> BinConfig:
+    cfg = BinConfig()
+    _check("gptoss_moe_bin_read_config",
+           load_library().gptoss_moe_bin_read_config(path.encode(), ctypes.byref(cfg)))
+    return cfg
+
+
+def bin_layer_offsets(cfg: BinConfig, layer: int) -> BinLayer:
+    o = BinLayer()
+    _check("gptoss_moe_bin_layer_offsets",
+           load_library().gptoss_moe_bin_layer_offsets(ctypes.byref(cfg), layer, ctypes.byref(o)))
+    return o

@@ -230,6 +230,52 @@ int gptoss_moe_pack_weights_fp4(const gptoss_moe_shape *shape, const gptoss_moe_
 int gptoss_moe_quantize_act(const uint16_t *x, int rows, int k_cols, int terms, uint8_t *q,
                             uint8_t *q_scales, hipStream_t stream);
 
+/* ---- the reference's fp32 checkpoint (.bin) ------------------------------ */
+/* Its header, the reference's Config (run.cpp:25-45), byte for byte. */
+typedef struct gptoss_moe_bin_config {
+    int vocab_size, hidden_dim, n_experts, experts_per_token, intermediate_dim, n_layers;
+    int head_dim, n_attn_heads, n_kv_heads, seq_len, initial_context_length;
+    float rope_theta, rope_scaling_factor;
+    int sliding_window;
+    float swiglu_limit;
+} gptoss_moe_bin_config;
+
+/* Byte offsets (from the start of the file) of one layer's MoE arrays, and
+ * the size the whole file must have (memory_map_weights, run.cpp:206-247). */
+typedef struct gptoss_moe_bin_layer {
+    int64_t rms_ffn_w, w_router, b_router, w_mlp1, b_mlp1, w_mlp2, b_mlp2, file_bytes;
+} gptoss_moe_bin_layer;
+
+/* Device destinations of gptoss_moe_load_bin_layer, in the layouts of
+ * gptoss_moe_weights (rms_ffn_w bf16 [H] may be NULL). */
+typedef struct gptoss_moe_bin_dest {
+    uint8_t *w1, *w1_scales;
+    uint16_t *b1;
+    uint8_t *w2, *w2_scales;
+    uint16_t *b2, *router_w, *router_b, *rms_ffn_w;
+} gptoss_moe_bin_dest;
+
+/* Reads the Config header of a checkpoint (host only). */
+int gptoss_moe_bin_read_config(const char *path, gptoss_moe_bin_config *cfg);
+
+/* Offsets of layer `layer` for a header (host only; no file access). */
+int gptoss_moe_bin_layer_offsets(const gptoss_moe_bin_config *cfg, int layer,
+                                 gptoss_moe_bin_layer *offsets);
+
+/*
+ * One layer's MoE weights from a checkpoint (the reference's GPU loader,
+ * getp_run.cpp:818-830 and :1140-1240): the file is memory-mapped; w_mlp1 and
+ * w_mlp2 go in chunks through the caller's staging (stage_host should be
+ * pinned, hipHostMalloc; stage_dev device memory; both stage_bytes, a multiple
+ * of 128, at least 4096) and are quantised on the device with the reference
+ * rule (gptoss_moe_quantize_mxfp4); router, biases and RMSNorm weight are
+ * rounded to bf16 on the host (__float2bfloat16, round to nearest even).
+ * Load-time only: synchronises the host with `stream` after every chunk.
+ */
+int gptoss_moe_load_bin_layer(const char *path, int layer, const gptoss_moe_bin_dest *dst,
+                              void *stage_host, void *stage_dev, size_t stage_bytes,
+                              hipStream_t stream);
+
 /* Last HIP error seen by this library on the calling thread (hipError_t). */
 int gptoss_moe_last_hip_error(void);
 
