@@ -103,6 +103,43 @@ def cpu_baseline(d, budget_s: float) -> dict:
                       f"(run.cpp:657-748 restated, fp32 weights = exact MXFP4 dequant), {dt:.1f} s"}
 
 
+def time_layer(layers, x, args):
+    """The whole moe_gpu layer (x += MoE(RMSNorm(x)), gptoss_moe_layer) with the
+    RMSNorm fused into the router kernel, beside the same work as a separate
+    RMSNorm launch + forward with the residual add."""
+    import numpy as np
+    import torch
+    import gptoss_moe
+    rng = np.random.default_rng(1)
+    import synth
+    rms_w = torch.from_numpy(synth.f32_to_bf16(
+        1 + 0.1 * rng.standard_normal(x.shape[1]).astype(np.float32)).view(np.int16)).to(x.device)
+    xs = x.clone()
+    t = torch.empty_like(x)
+
+    def run(fused):
+        for i in range(args.warmup + args.steps):
+            if i == args.warmup:
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+            xs.copy_(x)  # same input every step (the layer updates x in place)
+            L = layers[i % len(layers)]
+            if fused:
+                L.layer(xs, rms_w, t_scratch=t)
+            else:
+                gptoss_moe.rmsnorm(xs, rms_w, out=t)
+                L.forward(t, out=xs, residual=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+    fused, unfused = run(True), run(False)
+    return {"entry": "gptoss_moe_layer (RMSNorm fused into the router kernel, residual in finalize)",
+            "ms_per_step": round(fused, 5), "unfused_ms_per_step": round(unfused, 5),
+            "note": "both include a device copy of x per step (the layer updates x in place)"}
+
+
 def time_variants(layers, x, out, fi, fw, args, c, flops):
     """Extra measured variants (never the headline): the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
@@ -252,6 +289,8 @@ def main():
         "kernel_ms": {k: round(v, 5) for k, v in kms.items()},
         "wall_s_timed": round(wall, 4),
     }
+    if fi is None:
+        res["layer"] = time_layer(layers, x, args)
     if not args.no_variants:
         res["variants"] = time_variants(layers, x, out, fi, fw, args, c, flops)
     if not args.no_cpu:

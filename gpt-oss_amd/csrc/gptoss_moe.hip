@@ -219,22 +219,30 @@ int hist_block_tokens(int T) {
 // softmax over the K selected.  With forced routing the given indices and
 // weights are validated and copied instead (invalid or repeated experts are
 // dropped).  slot_e[t][k] = expert of a live slot, -1 for a dropped one.
+//
+// With rms_w (the layer entry point) the staged rows are first replaced by
+// t = RMSNorm(x; rms_w), computed exactly as rmsnorm_kernel (the pre-MoE
+// RMSNorm, rmsnorm.hpp:113-164, fused here): thread tid's double partial over
+// i = tid, tid + 256, ..., a halving tree, inv = 1 / sqrt(mean + 1e-5) in
+// double, t = bf16(w * (float(inv) * x)); t goes to t_out for the GEMMs.
 template <int TB, int EE>
 __global__ __launch_bounds__(256) void route_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ wr,
     const uint16_t *__restrict__ br, const int32_t *__restrict__ forced_i,
     const uint16_t *__restrict__ forced_w, int T, int H, int E, int K, int nthreads_ref,
     int block_tokens, uint16_t *__restrict__ logits, int32_t *__restrict__ topk_i,
-    uint16_t *__restrict__ topk_w, int32_t *__restrict__ slot_e, int32_t *__restrict__ hist) {
+    uint16_t *__restrict__ topk_w, int32_t *__restrict__ slot_e, int32_t *__restrict__ hist,
+    const uint16_t *__restrict__ rms_w, uint16_t *__restrict__ t_out) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[TB * kMaxHidden];
     __shared__ float sc[TB][kMaxExperts];
+    __shared__ double ssq[TB][256];
     __shared__ int shist[kHistCols];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.x * TB;
     const int nt = min(TB, T - t0);
     for (int c = tid; c <= E; c += 256) shist[c] = 0;
 
-    if (forced_i == nullptr) {
+    if (forced_i == nullptr || rms_w != nullptr) {
         // ---- stage the x rows (rows past T repeat the last token); every
         // load is issued before the first store
         const int h8 = H / 8, n8 = TB * h8;
@@ -252,6 +260,59 @@ __global__ __launch_bounds__(256) void route_kernel(
             if (i < n8) *reinterpret_cast<uint4 *>(&xs[8 * i]) = v[u];
         }
         __syncthreads();
+    }
+    if (rms_w != nullptr) {
+        // ---- fused pre-MoE RMSNorm of the staged rows
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt) {
+            double s = 0.0;
+            for (int i = tid; i < H; i += 256) {
+                const double v = (double)bf2f(xs[tt * H + i]);
+                s = __dadd_rn(s, __dmul_rn(v, v));
+            }
+            ssq[tt][tid] = s;
+        }
+        __syncthreads();
+        // the halving tree s[i] += s[i + st], st = 128 .. 1: the two cross-wave
+        // levels in LDS, then wave 0's 64 lanes with lane moves (the same pairs)
+        if (tid < 128)
+#pragma unroll
+            for (int tt = 0; tt < TB; ++tt) ssq[tt][tid] = __dadd_rn(ssq[tt][tid], ssq[tt][tid + 128]);
+        __syncthreads();
+        if (tid < 64) {
+#pragma unroll
+            for (int tt = 0; tt < TB; ++tt) {
+                double v = __dadd_rn(ssq[tt][tid], ssq[tt][tid + 64]);
+                auto down = [&](auto st_c) {
+                    constexpr int st = decltype(st_c)::value;
+                    const uint64_t b = __double_as_longlong(v);
+                    const uint32_t lo = (uint32_t)down64<st>((int)(uint32_t)b);
+                    const uint32_t hi = (uint32_t)down64<st>((int)(uint32_t)(b >> 32));
+                    const double o = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+                    if (lane < st) v = __dadd_rn(v, o);
+                };
+                down(std::integral_constant<int, 32>());
+                down(std::integral_constant<int, 16>());
+                down(std::integral_constant<int, 8>());
+                down(std::integral_constant<int, 4>());
+                down(std::integral_constant<int, 2>());
+                down(std::integral_constant<int, 1>());
+                if (lane == 0) ssq[tt][0] = v;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt) {
+            const float invf = (float)(1.0 / sqrt(ssq[tt][0] / (double)H + 1e-5));
+            for (int i = tid; i < H; i += 256) {
+                const uint16_t tv = f2bf(__fmul_rn(bf2f(rms_w[i]), __fmul_rn(invf, bf2f(xs[tt * H + i]))));
+                xs[tt * H + i] = tv;
+                if (tt < nt) t_out[(size_t)(t0 + tt) * H + i] = tv;
+            }
+        }
+        lds_barrier();  // xs normalised; the t_out stores need not have landed
+    }
+    if (forced_i == nullptr) {
 
         // ---- logits
         const int l16 = tid & 15, grp = tid >> 4;
@@ -2569,28 +2630,34 @@ struct Marks {
 template <int TB, int EE>
 void launch_route_kernel(const gptoss_moe_shape *s, const gptoss_moe_weights *w,
                          const uint16_t *x, int T, const int32_t *fi, const uint16_t *fw,
-                         int nthreads_ref, int bt, const Ptrs &p, hipStream_t st) {
+                         int nthreads_ref, int bt, const Ptrs &p, hipStream_t st,
+                         const uint16_t *rms_w, uint16_t *t_out) {
     hipLaunchKernelGGL((route_kernel<TB, EE>), dim3((T + TB - 1) / TB), dim3(256), 0, st, x,
                        w->router_w, w->router_b, fi, fw, T, s->hidden, s->n_experts, s->top_k,
-                       nthreads_ref, bt, p.logits, p.topk_i, p.topk_w, p.slot_e, p.hist);
+                       nthreads_ref, bt, p.logits, p.topk_i, p.topk_w, p.slot_e, p.hist, rms_w,
+                       t_out);
 }
 
 template <int TB>
 void launch_route_tb(int ee, const gptoss_moe_shape *s, const gptoss_moe_weights *w,
                      const uint16_t *x, int T, const int32_t *fi, const uint16_t *fw,
-                     int nthreads_ref, int bt, const Ptrs &p, hipStream_t st) {
+                     int nthreads_ref, int bt, const Ptrs &p, hipStream_t st,
+                     const uint16_t *rms_w, uint16_t *t_out) {
     switch (ee) {
-    case 1: launch_route_kernel<TB, 1>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
-    case 2: launch_route_kernel<TB, 2>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
-    case 4: launch_route_kernel<TB, 4>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
-    case 8: launch_route_kernel<TB, 8>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st); break;
-    default: launch_route_kernel<TB, (TB > 4 ? 8 : 16)>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+    case 1: launch_route_kernel<TB, 1>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out); break;
+    case 2: launch_route_kernel<TB, 2>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out); break;
+    case 4: launch_route_kernel<TB, 4>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out); break;
+    case 8: launch_route_kernel<TB, 8>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out); break;
+    default:
+        launch_route_kernel<TB, (TB > 4 ? 8 : 16)>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st,
+                                                    rms_w, t_out);
     }
 }
 
 int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                  int T, const int32_t *fi, const uint16_t *fw, const Ptrs &p, hipStream_t st,
-                 int tile_rows, bool gather, Marks *mk = nullptr) {
+                 int tile_rows, bool gather, Marks *mk = nullptr,
+                 const uint16_t *rms_w = nullptr, uint16_t *t_out = nullptr) {
     int nthreads_ref = 1;
     while (nthreads_ref < s->n_experts) nthreads_ref <<= 1;
     nthreads_ref = nthreads_ref < 64 ? 64 : (nthreads_ref > 512 ? 512 : nthreads_ref);
@@ -2604,13 +2671,14 @@ int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const u
     if (ee == 16 && tb == 8) tb = 4;
     if (fi != nullptr) tb = 8;  // no router GEMM
     if (tb == 8 && fi != nullptr)
-        launch_route_kernel<8, 1>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+        launch_route_kernel<8, 1>(s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out);
     else if (tb == 8)
-        launch_route_tb<8>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+        launch_route_tb<8>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out);
     else if (tb == 4)
-        launch_route_tb<4>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+        launch_route_tb<4>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out);
     else
-        launch_route_tb<1>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st);
+        launch_route_tb<1>(ee, s, w, x, T, fi, fw, nthreads_ref, bt, p, st, rms_w, t_out);
+    if (rms_w != nullptr) x = t_out;  // the index kernel gathers normalised rows
     if (mk) mk->mark(st);
     int G = 8 * device_cus() / n_blk;
     G = G < 1 ? 1 : (G > 256 ? 256 : G);
@@ -2884,12 +2952,19 @@ int gptoss_moe_layer(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
     if (!rms_w || !x || !t_scratch) return GPTOSS_MOE_ERR_INVALID_ARG;
     int rc = check_common(shape, w, n_tokens, nullptr, nullptr, workspace, ws_bytes, max_tokens);
     if (rc) return rc;
+    if ((rc = check_experts(w, 0)) != 0) return rc;
     if (n_tokens == 0) return GPTOSS_MOE_OK;
-    rc = gptoss_moe_rmsnorm(x, rms_w, t_scratch, n_tokens, shape->hidden, stream);
+    if (!aligned16(x) || !aligned16(t_scratch)) return GPTOSS_MOE_ERR_INVALID_ARG;
+    // RMSNorm fused into the router kernel (t_scratch = RMSNorm(x)), the GEMMs
+    // on t_scratch, the residual add in the finalize kernel
+    const WsLayout L = ws_layout(*shape, max_tokens);
+    const Ptrs p = ws_ptrs(L, workspace);
+    rc = launch_route(shape, w, x, n_tokens, nullptr, nullptr, p, stream,
+                      gemm_tile_rows(shape, w, n_tokens, 0),
+                      gemm_path(shape, w, n_tokens, 0) < PATH_DIRECT, nullptr, rms_w, t_scratch);
     if (rc) return rc;
-    return gptoss_moe_forward(shape, w, t_scratch, x, n_tokens, nullptr, nullptr,
-                              GPTOSS_MOE_FLAG_RESIDUAL_ADD, workspace, ws_bytes, max_tokens,
-                              stream);
+    return launch_experts(shape, w, t_scratch, x, n_tokens, GPTOSS_MOE_FLAG_RESIDUAL_ADD, L, p,
+                          stream);
 }
 
 int gptoss_moe_dequant_mxfp4(const uint8_t *packed, const uint8_t *scales, int n_experts,

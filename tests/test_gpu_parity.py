@@ -328,19 +328,43 @@ def test_rmsnorm_bit_exact(gpu):
     assert np.array_equal(got, oracle.rmsnorm(x, w))
 
 
-def test_layer_matches_oracle(gpu):
+@pytest.mark.parametrize("name", ["c1_20b_decode", "c0_tiny", "c3a_120b_decode"])
+def test_layer_matches_oracle(gpu, name):
     """moe_gpu at TP = 1: RMSNorm -> MoE -> residual add, in place."""
+    import torch
     import gptoss_moe
-    d = _data("c1_20b_decode")
+    d = _data(name)
     rng = np.random.default_rng(9)
     rms_w = synth.f32_to_bf16(1 + 0.1 * rng.standard_normal(d.cfg.hidden).astype(np.float32))
     layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
     x = _dev(d.x, gpu)
-    layer.layer(x, _dev(rms_w, gpu))
+    t_scratch = torch.empty_like(x)
+    layer.layer(x, _dev(rms_w, gpu), t_scratch=t_scratch)
     t = oracle.rmsnorm(d.x, rms_w)
+    # the RMSNorm fused into the router kernel is bit-exact
+    assert np.array_equal(_host16(t_scratch), t)
     e = oracle.moe_forward(d, x_norm=t, forced=False)["e_agg"]
     want = oracle.residual_add(d.x, e)
     assert_close(_host16(x), want, "layer")
+
+
+def test_layer_prefill_sampled(gpu):
+    """The layer at 4096 tokens (8 tokens per router workgroup): the fused
+    RMSNorm bit-exact on every row, the output on sampled rows."""
+    import torch
+    import gptoss_moe
+    d = _data("c3b_120b_prefill")
+    rng = np.random.default_rng(10)
+    rms_w = synth.f32_to_bf16(1 + 0.1 * rng.standard_normal(d.cfg.hidden).astype(np.float32))
+    layer = gptoss_moe.MoeLayer.from_numpy(d, device=gpu)
+    x = _dev(d.x, gpu)
+    t_scratch = torch.empty_like(x)
+    layer.layer(x, _dev(rms_w, gpu), t_scratch=t_scratch)
+    t = oracle.rmsnorm(d.x, rms_w)
+    assert np.array_equal(_host16(t_scratch), t)
+    rows = np.sort(rng.choice(d.cfg.tokens, 128, replace=False))
+    e = oracle.moe_forward(d, x_norm=t, forced=False, rows=rows)["e_agg"]
+    assert_close(_host16(x)[rows], oracle.residual_add(d.x[rows], e), "layer c3b")
 
 
 def test_zero_tokens_is_noop(gpu):
