@@ -77,10 +77,12 @@ def test_argument_errors_without_gpu():
     w.router_w = w.router_b = 1 << 20
     assert lib.gptoss_moe_route(ctypes.byref(s), ctypes.byref(w), None, 4, None, None, fake,
                                 64, 8, None) == gm.ERR_WORKSPACE
-    # unknown flag bits
+    # unknown flag bits; the FP4 variant's flags without its weights or combined wrongly
     need = gm.workspace_size(s, 8)
-    assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
-                                  8, fake, need, 8, None) == gm.ERR_INVALID_ARG
+    for flags in (64, gm.FLAG_FP4_MFMA, gm.FLAG_FP8_ACT,
+                  gm.FLAG_FP4_MFMA | gm.FLAG_SMALL_M_GEMM):
+        assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
+                                      flags, fake, need, 8, None) == gm.ERR_INVALID_ARG, flags
     # hidden beyond the supported envelope (LDS staging of router rows and scale blocks)
     big = gm.make_shape(3072 + 64, 128, 4, 2)
     assert lib.gptoss_moe_route(ctypes.byref(big), ctypes.byref(w), None, 4, None, None, fake,
@@ -92,3 +94,14 @@ def test_argument_errors_without_gpu():
     assert lib.gptoss_moe_quantize_mxfp4(None, 0, None, None, None) == gm.OK
     assert lib.gptoss_moe_pack_weights(None, None, None, 0, None) == gm.ERR_INVALID_ARG
     assert lib.gptoss_moe_packed_size(None) == 0
+    assert lib.gptoss_moe_pack_weights_fp4(None, None, None, 0, None) == gm.ERR_INVALID_ARG
+    # quantize_act: K a multiple of 8, terms 1 or 2, 16-byte aligned x, 8-byte aligned codes
+    assert lib.gptoss_moe_quantize_act(fake, 4, 100, 2, fake, fake, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_act(fake, 4, 128, 3, fake, fake, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_act(None, 4, 128, 2, fake, fake, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_act(ctypes.c_void_p((1 << 20) + 8), 4, 128, 2, fake, fake,
+                                       None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_quantize_act(None, 0, 128, 2, None, None, None) == gm.OK
+    assert lib.gptoss_moe_bin_read_config(None, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_bin_layer_offsets(None, 0, None) == gm.ERR_INVALID_ARG
+    assert lib.gptoss_moe_load_bin_layer(None, 0, None, None, None, 0, None) == gm.ERR_INVALID_ARG
