@@ -1752,11 +1752,6 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
-__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
-    u32x4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
 template <int OFF>
 __device__ __forceinline__ u32x4 lds_read_b128_at(uint32_t addr) {
     u32x4 v;
