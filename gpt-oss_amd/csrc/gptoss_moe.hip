@@ -852,13 +852,16 @@ __device__ __forceinline__ int lds_row_of(int wr) {
     return kMlp1 ? ((wr & 1) << 4) | (wr >> 1) : wr;
 }
 
-// Work items are (tile, 128-row weight block).  Workgroups are dispatched to
-// the 8 XCDs round robin (workgroup b runs on XCD b % 8) and the tile list is
+// Work items are (tile, weight block).  Workgroups are dispatched to the 8
+// XCDs round robin (workgroup b runs on XCD b % 8) and the tile list is
 // grouped by XCD, so XCD x only touches its own tiles: their activation rows
 // stay in its L2, and the tiles of one expert (one unit) stream each weight
-// block from the same L2.  Within an XCD, items are weight-block-major
-// (consecutive items are the XCD's tiles at one block), and its Gx
-// workgroups stride over them.
+// block from the same L2.  Within an XCD, items are tile-major (consecutive
+// items are the blocks of one tile), and its Gx workgroups stride over them:
+// the workgroups running at one time stream neighbouring blocks of one
+// expert's weights, contiguous in memory, and share the tile's activation
+// rows.  (Block-major order, where they stream one block of many experts
+// spread over the whole weight array, was 7-11% slower at decode.)
 struct ItemMap {
     int nblk, xcd, w, Gx, base, ntx;
     __device__ __forceinline__ void init(const int32_t *hdr, int nblk_, int &n_items) {
@@ -877,9 +880,10 @@ struct ItemMap {
     // no kernel that reads it writes it.
     __device__ __forceinline__ void at(const Tile *tiles, int i, Tile &tl, int &nb) const {
         const int ii = w + i * Gx;
-        nb = ii / ntx;
+        const int tli = ii / nblk;
+        nb = ii - tli * nblk;
         typedef const __attribute__((address_space(4))) int32_t *ConstInts;
-        const ConstInts t = (ConstInts)(tiles + base + ii - nb * ntx);
+        const ConstInts t = (ConstInts)(tiles + base + tli);
         tl.expert = t[0];
         tl.row0 = t[1];
         tl.rows = t[2];
