@@ -2,16 +2,20 @@
 //
 // Kernels (one stream, no host round trip):
 //   route_kernel   router GEMM in a pinned fp32 order (bit-reproducible)
-//                  fused with top-k/softmax; per-block expert histogram.
-//   plan_kernel    counts, offsets, per-block row bases, tile list.
-//   index_gather_kernel  compact row -> token map; x rows gathered into
-//                  compact order.
-//   mlp1_kernel    grouped GEMM x[token(row)] . W1[e]^T, MXFP4 dequantised
-//                  in registers (v_cvt_scalef32_pk_bf16_fp4) into bf16 MFMA
-//                  operands; epilogue: bias + clamped SwiGLU on the
-//                  interleaved gate/up rows, bf16 out.
-//   mlp2_kernel    grouped GEMM act . W2[e]^T; epilogue: bias, bf16 round,
-//                  scatter of each row to its token-order slot [t][k][h].
+//                  fused with top-k/softmax (and, for the layer entry point,
+//                  the pre-MoE RMSNorm); per-block expert histogram.
+//   index_kernel   histogram scan (counts, offsets, the XCD-grouped tile
+//                  list), compact row -> token map, and for the LDS-staged
+//                  GEMMs the gather of x rows into compact order.
+//   direct_gemm_kernel<true>   MLP1 on the packed weights: x rows read
+//                  through the row map, MXFP4 dequantised in registers
+//                  (v_cvt_scalef32_pk_bf16_fp4) into bf16 MFMA operands;
+//                  epilogue: bias + clamped SwiGLU on the interleaved
+//                  gate/up rows, bf16 out.
+//   direct_gemm_kernel<false>  MLP2 (act . W2[e]^T); epilogue: bias, bf16
+//                  round, each row to its token-order slot [t][k][h].
+//   grouped_gemm_kernel / large_m_gemm_kernel  the same two GEMMs on the
+//                  reference weight layout (no packed copy).
 //   finalize_kernel  router-weighted k-way sum of the slots in slot order
 //                  (fmaf, fp32) -> bf16, optionally + residual.
 //
