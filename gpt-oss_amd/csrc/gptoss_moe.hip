@@ -24,6 +24,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "../../include/gptoss_moe.h"
@@ -2542,17 +2543,19 @@ int hip_status(hipError_t err) {
     return GPTOSS_MOE_ERR_HIP;
 }
 
+// CU count of the current device, cached per device (host threads may race
+// on the first query; they store the same value).
 int device_cus() {
-    static int cus[64] = {0};
+    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int v = 0;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
             v = 256;
-        cus[dev] = v;
+        cus[dev].store(v, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return v;
 }
 
 bool shape_ok(const gptoss_moe_shape *s) {
