@@ -301,6 +301,25 @@ class MoeLayer:
         _check("gptoss_moe_forward", rc)
         return out
 
+    def capture_forward(self, x_norm, out, forced_i=None, forced_w=None, residual=False,
+                        path="auto"):
+        """A HIP graph of one forward() on these buffers (a torch.cuda.CUDAGraph:
+        .replay() reruns the same kernels on whatever the buffers then hold).
+        A call allocates nothing, issues no memset and does not synchronise, so
+        the captured launches are exactly the eager ones; the routing histogram
+        is cleared by each call's index kernel, so replays and eager calls on the
+        same workspace may interleave (stream-ordered, never concurrently)."""
+        import torch
+        side = torch.cuda.Stream()  # warm-up off the capture stream, default priority
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.forward(x_norm, out, forced_i, forced_w, residual, path=path)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.forward(x_norm, out, forced_i, forced_w, residual, path=path)
+        return graph
+
     KERNELS = ("route", "index", "mlp1", "mlp2", "finalize")
 
     def forward_profiled(self, x_norm, out, forced_i=None, forced_w=None, stream=None,
