@@ -272,3 +272,34 @@ def test_tile_placement_64_rows(seed):
     placed, xcount, unit_xcd = build_tiles(counts, tile_rows=64)
     assert sorted(placed) == list(range(sum((c + 63) // 64 for c in counts)))
     assert max(xcount) - min(xcount) <= 2
+
+
+# ------------------------------------------------------------ work items --
+def item_map(ntx, nblk, Gx):
+    """ItemMap.init / ItemMap.at for one XCD: workgroup w runs items
+    ii = w + i Gx (i < n_items), item ii = (tile ii / nblk, block ii % nblk)."""
+    items_x = ntx * nblk
+    per_wg = []
+    for w in range(Gx):
+        n_items = (items_x - w + Gx - 1) // Gx if items_x > w else 0
+        got = []
+        for i in range(n_items):
+            ii = w + i * Gx
+            tli = ii // nblk
+            got.append((tli, ii - tli * nblk))
+        per_wg.append(got)
+    return per_wg
+
+
+@pytest.mark.parametrize("ntx,nblk,Gx", [(4, 23, 32), (4, 12, 32), (16, 23, 32), (1, 1, 32),
+                                         (0, 12, 32), (3, 45, 64), (33, 12, 32), (5, 7, 3)])
+def test_items_cover_every_tile_block_once(ntx, nblk, Gx):
+    per_wg = item_map(ntx, nblk, Gx)
+    flat = [it for got in per_wg for it in got]
+    assert sorted(flat) == [(t, b) for t in range(ntx) for b in range(nblk)]
+    # tile-major: the workgroups' first items are consecutive blocks of the first tiles
+    first = [got[0] for got in per_wg if got]
+    assert first == sorted(first)
+    # balanced: item counts per workgroup differ by at most one
+    n = [len(got) for got in per_wg]
+    assert max(n) - min(n) <= 1
