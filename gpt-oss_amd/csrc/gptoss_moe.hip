@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/gptoss_moe.h"
@@ -2845,6 +2846,59 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     return hip_status(hipGetLastError());
 }
 
+
+// ------------------------------------------------- no-allocation scratch --
+// gptoss_moe_forward_noalloc runs on this file-scope device array instead of
+// a caller workspace.  Each GPU the library runs on holds its own copy until
+// the process ends.  Host code never passes `scratch` itself to a kernel: the
+// name is a host-side stand-in, and the array's device address on the
+// current device comes from hipGetSymbolAddress (scratch_ptr below).
+constexpr size_t kScratchBytes = (size_t)128 << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Zero the workspace header and routing histogram (the state a call expects
+// at entry; every call leaves them zero again).  A kernel rather than
+// hipMemsetAsync, so callers may capture the first call in a HIP graph.
+__global__ __launch_bounds__(256) void zero_kernel(int32_t *__restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        p[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device (nullptr: not set up)
+bool g_scratch_zeroed[kMaxDevices];
+
+// Address of the current device's `scratch`, set up once per device (with the
+// device current): symbol lookup, then the header + histogram cleared on
+// `stream` before the first call's kernels.
+int scratch_ptr(void **out, hipStream_t stream) {
+    int dev = 0;
+    int rc = hip_status(hipGetDevice(&dev));
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return GPTOSS_MOE_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *ptr = nullptr;
+        rc = hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (rc) return rc;
+        if (ptr == nullptr) return GPTOSS_MOE_ERR_HIP;
+        g_scratch_ptr[dev] = ptr;
+    }
+    if (!g_scratch_zeroed[dev]) {
+        // hdr and hist sit at the front of every layout, at offsets that do
+        // not depend on the shape or the token count
+        const size_t n_ints = (size_t)(HDR_INTS + kMaxBlocks * kHistCols);
+        hipLaunchKernelGGL(zero_kernel, dim3(64), dim3(256), 0, stream,
+                           static_cast<int32_t *>(g_scratch_ptr[dev]), n_ints);
+        rc = hip_status(hipGetLastError());
+        if (rc) return rc;
+        g_scratch_zeroed[dev] = true;
+    }
+    *out = g_scratch_ptr[dev];
+    return GPTOSS_MOE_OK;
+}
+
 }  // namespace
 
 // ================================================================ C ABI ==
@@ -2914,6 +2968,23 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     if (rc) return rc;
     return launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream);
 }
+
+int gptoss_moe_forward_noalloc(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                               const uint16_t *x_norm, uint16_t *out, int n_tokens,
+                               const int32_t *forced_topk_i, const uint16_t *forced_topk_w,
+                               unsigned flags, hipStream_t stream) {
+    if (!shape_ok(shape) || n_tokens < 0) return GPTOSS_MOE_ERR_INVALID_ARG;
+    // the workspace this call needs, laid out for exactly n_tokens
+    const size_t need = ws_layout(*shape, n_tokens).total;
+    if (need > kScratchBytes) return GPTOSS_MOE_ERR_WORKSPACE;
+    void *ws = nullptr;
+    int rc = scratch_ptr(&ws, stream);
+    if (rc) return rc;
+    return gptoss_moe_forward(shape, w, x_norm, out, n_tokens, forced_topk_i, forced_topk_w, flags,
+                              ws, kScratchBytes, n_tokens, stream);
+}
+
+size_t gptoss_moe_noalloc_max_bytes(void) { return kScratchBytes; }
 
 int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
                                 const uint16_t *x_norm, uint16_t *out, int n_tokens,

@@ -101,6 +101,10 @@ _SIGS = {
     "gptoss_moe_forward": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights), _VP, _VP,
                                           ctypes.c_int, _VP, _VP, ctypes.c_uint, _VP,
                                           ctypes.c_size_t, ctypes.c_int, _VP]),
+    "gptoss_moe_forward_noalloc": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights),
+                                                  _VP, _VP, ctypes.c_int, _VP, _VP, ctypes.c_uint,
+                                                  _VP]),
+    "gptoss_moe_noalloc_max_bytes": (ctypes.c_size_t, []),
     "gptoss_moe_route": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(Weights), _VP,
                                         ctypes.c_int, _VP, _VP, _VP, ctypes.c_size_t,
                                         ctypes.c_int, _VP]),
@@ -299,6 +303,22 @@ class MoeLayer:
             (FLAG_RESIDUAL_ADD if residual else 0) | _PATH_FLAGS[path],
             self.ws.data_ptr(), self.ws_bytes, self.max_tokens, _stream(stream))
         _check("gptoss_moe_forward", rc)
+        return out
+
+    def forward_noalloc(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,
+                        stream=None, path="auto"):
+        """forward() on the library's per-GPU device array instead of this
+        layer's workspace (gptoss_moe_forward_noalloc: no allocation in the
+        call; calls that overlap on one GPU race)."""
+        import torch
+        T = x_norm.shape[0]
+        if out is None:
+            out = torch.empty_like(x_norm)
+        rc = self.lib.gptoss_moe_forward_noalloc(
+            ctypes.byref(self.shape), ctypes.byref(self.w), _ptr(x_norm), _ptr(out), T,
+            _ptr(forced_i), _ptr(forced_w),
+            (FLAG_RESIDUAL_ADD if residual else 0) | _PATH_FLAGS[path], _stream(stream))
+        _check("gptoss_moe_forward_noalloc", rc)
         return out
 
     def capture_forward(self, x_norm, out, forced_i=None, forced_w=None, residual=False,

@@ -141,6 +141,26 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
                        hipStream_t stream);
 
 /*
+ * gptoss_moe_forward without a caller workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The workspace is a
+ * file-scope device array of gptoss_moe_noalloc_max_bytes() bytes (128 MiB),
+ * one per GPU, held until the process ends; the first call on a device looks
+ * up its address and clears its routing state with a small kernel on
+ * `stream`.  The call allocates nothing and returns GPTOSS_MOE_ERR_WORKSPACE
+ * when gptoss_moe_workspace_size(shape, n_tokens) exceeds the array (20B
+ * shape, k = 4: up to about 1300 tokens).  Every call on one GPU shares its
+ * array: calls that overlap on one GPU (different streams or host threads
+ * without ordering) race.  Results equal gptoss_moe_forward's.
+ */
+int gptoss_moe_forward_noalloc(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
+                               const uint16_t *x_norm, uint16_t *out, int n_tokens,
+                               const int32_t *forced_topk_i, const uint16_t *forced_topk_w,
+                               unsigned flags, hipStream_t stream);
+/* Size of the device array gptoss_moe_forward_noalloc works in. */
+size_t gptoss_moe_noalloc_max_bytes(void);
+
+/*
  * Routing only (router GEMM, top-k + softmax, histogram, prefix, row map):
  * the first half of gptoss_moe_forward, leaving its results in the workspace
  * (see gptoss_moe_workspace_views).  Replaces getp_run.cpp:2609-2732.

@@ -105,3 +105,21 @@ def test_argument_errors_without_gpu():
     assert lib.gptoss_moe_bin_read_config(None, None) == gm.ERR_INVALID_ARG
     assert lib.gptoss_moe_bin_layer_offsets(None, 0, None) == gm.ERR_INVALID_ARG
     assert lib.gptoss_moe_load_bin_layer(None, 0, None, None, None, 0, None) == gm.ERR_INVALID_ARG
+
+
+def test_noalloc_rejects_without_gpu_work():
+    """gptoss_moe_forward_noalloc checks the shape and the size its device
+    array holds before any HIP call."""
+    lib = gm.load_library()
+    assert lib.gptoss_moe_noalloc_max_bytes() == 128 << 20
+    w = gm.Weights()
+    bad = gm.make_shape(2880, 100, 32, 4)
+    assert lib.gptoss_moe_forward_noalloc(ctypes.byref(bad), ctypes.byref(w), None, None, 4,
+                                          None, None, 0, None) == gm.ERR_INVALID_ARG
+    s20 = gm.make_shape(2880, 2880, 32, 4)
+    big = 20000  # far beyond what 128 MiB holds at this shape
+    assert gm.workspace_size(s20, big) > lib.gptoss_moe_noalloc_max_bytes()
+    assert lib.gptoss_moe_forward_noalloc(ctypes.byref(s20), ctypes.byref(w), None, None, big,
+                                          None, None, 0, None) == gm.ERR_WORKSPACE
+    assert lib.gptoss_moe_forward_noalloc(ctypes.byref(s20), ctypes.byref(w), None, None, -1,
+                                          None, None, 0, None) == gm.ERR_INVALID_ARG
