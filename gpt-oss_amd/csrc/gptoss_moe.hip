@@ -961,11 +961,7 @@ __device__ __forceinline__ void gemm_wproducer(const GemmArgs &a, StageSlot *slo
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint32_t el = el0 + t * 8u * (uint32_t)K;
-#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 1)
-                q[r][4 * hh + t] = make_uint4(el, el, 0, 0);  // timing diagnostic: no weight loads
-#else
                 q[r][4 * hh + t] = *reinterpret_cast<const uint4 *>(wq + el / 2);
-#endif
             }
         }
         stage_of[r] = j;
@@ -1048,11 +1044,7 @@ __device__ __forceinline__ void gemm_aloader(const GemmArgs &a, StageSlot *slots
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t off = (uint32_t)min(4 * i + 2 * p + (lane >> 5), rmax) * (2u * K) + kb;
-#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 2)
-            v[r][i] = u32x4{off, 0u, 0u, 0u};  // timing diagnostic: no activation loads
-#else
             v[r][i] = *reinterpret_cast<const u32x4 *>(base + off);
-#endif
         }
     };
 #pragma unroll
@@ -1404,11 +1396,7 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
             const int q = tid + 512 * i, row = q >> 4, u = q & 15;
             const uint32_t off = (uint32_t)min(row, tl.rows - 1) * (2u * K) +
                                  2u * (uint32_t)min(j * kLBK + 8 * u, K - 8);
-#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 2)
-            ra[r][i] = u32x4{off, 0u, 0u, 0u};  // timing diagnostic: no activation loads
-#else
             ra[r][i] = *reinterpret_cast<const u32x4 *>(abase + off);
-#endif
         }
         const uint8_t *wq = a.Wq + (size_t)tl.expert * ((size_t)N * K / 2);
 #pragma unroll
@@ -1416,11 +1404,7 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
             const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
             const uint32_t row = (uint32_t)min(nb * kLBN + r0, N - 1);
             const uint32_t kb = (uint32_t)min(j * (kLBK / 2) + 16 * u, K / 2 - 16);
-#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 1)
-            rb[r][i] = u32x4{row, kb, 0u, 0u};  // timing diagnostic: no weight loads
-#else
             rb[r][i] = *reinterpret_cast<const u32x4 *>(wq + row * (uint32_t)(K / 2) + kb);
-#endif
         }
         // waves 0..3: scales of block row tid; 4, 5: bias pair; 6, 7: token slot
         const uint16_t *p16;
@@ -1506,11 +1490,7 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
                     const uint32_t zm = e == 0 ? 0x88888888u : 0xffffffffu;
                     const uint4 v = bw[c][s >> 2];
                     const uint32_t dw = (s & 3) == 0 ? v.x : (s & 3) == 1 ? v.y : (s & 3) == 2 ? v.z : v.w;
-#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 4)
-                    bq[c] = __builtin_bit_cast(bf16x8, u32x4{dw, dw ^ zm, e, dw ^ 3u});  // timing diagnostic
-#else
                     bq[c] = dequant8(dw & zm, e8m0_to_f32(e));
-#endif
                 }
 #pragma unroll
                 for (int f = 0; f < 2; ++f) {
@@ -1519,12 +1499,7 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
                         const bf16x8 av = __builtin_bit_cast(bf16x8, sb.a[row * 16 + ((8 * g + s) ^ (row & 15))]);
 #pragma unroll
                         for (int c = 0; c < 2; ++c) {
-#if defined(GPTOSS_DIAG) && (GPTOSS_DIAG & 8)
-                            const u32x4 x0 = __builtin_bit_cast(u32x4, av), y0 = __builtin_bit_cast(u32x4, bq[c]);
-                            acc[f][c][0] += __uint_as_float((x0.x ^ y0.y ^ x0.z ^ y0.w) & 0x3fffffffu);  // timing diagnostic
-#else
                             acc[f][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bq[c], acc[f][c], 0, 0, 0);
-#endif
                         }
                     }
                 }
@@ -1674,11 +1649,28 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
             if (byte < K / 2)
                 v = *reinterpret_cast<const uint32_t *>(wq + ((size_t)e * N + row) * (K / 2) + byte);
             pw[i] = v;
+        } else if (fmt == 0) {
+            // [e][kp][ct][16 rows][4 B]: byte i of row n = group 4 kp + i;
+            // zero past K / 32 and past the layout (the region is sized for fmt 1)
+            const size_t b = i - nw;
+            uint8_t v = 0;
+            if (b < (size_t)E * KP * CT * 64) {
+                const int gi = (int)(b & 3), n = (int)((b >> 2) & 15);
+                size_t r = b >> 6;
+                const int ct = (int)(r % CT);
+                r /= CT;
+                const int kp = (int)(r % KP);
+                const int e = (int)(r / KP);
+                const int row = packed_src_row(16 * ct + n, mlp1 != 0);
+                const int grp = 4 * kp + gi;
+                if (grp < KS) v = ws[((size_t)e * N + row) * KS + grp];
+            }
+            ps[b] = v;
         } else {
             const size_t b = i - nw;
-            // fmt 0: byte (n, gi) = row n, group gi; fmt 1: lane (n, g), byte bb -> group 4 bb + g
-            const int n = fmt == 0 ? (int)((b >> 4) & 15) : (int)((b >> 2) & 15);
-            const int gi = fmt == 0 ? (int)(b & 15) : (int)(4 * (b & 3) + ((b >> 6) & 3));
+            // fmt 1: lane (n, g), byte bb -> group 4 bb + g
+            const int n = (int)((b >> 2) & 15);
+            const int gi = (int)(4 * (b & 3) + ((b >> 6) & 3));
             size_t r = b >> 8;
             const int kq = (int)(r % KQ);
             r /= KQ;
@@ -2289,6 +2281,382 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
 #undef DTR
 }
 
+// ------------------------------------------------- streamed expert GEMM --
+//
+// The default MLP1 / MLP2 GEMM on packed weights.  One workgroup of 12 waves
+// per CU, persistent, with the waves specialised so that HBM streaming never
+// waits on compute:
+//   waves 0..7   consumers: LDS only.  Consumer c owns weight unit c of the
+//                item (2 MFMA column tiles = 32 weight rows): dequantises its
+//                nibbles (v_cvt_scalef32_pk_bf16_fp4 with the e8m0 fix-ups)
+//                and runs v_mfma_f32_16x16x32_bf16 against the tile's
+//                activation rows, then the epilogue (bias + clamped SwiGLU
+//                for MLP1, bias + token-order slot for MLP2).
+//   waves 8, 9   weight producers: nontemporal global -> LDS loads (1 KB per
+//                instruction) of the item's packed nibbles (8 column tiles
+//                each), the stage's e8m0 block (wave 8) and the item's biases
+//                and row slots (wave 9), kSDW - 1 stages ahead.
+//   waves 10, 11 activation producers: global -> LDS loads of the tile's
+//                activation rows (32 rows each, x rows by token for MLP1),
+//                kSDA - 1 stages ahead.
+// A stage is 128 k of one item.  Iteration s: each producer waits until its
+// own loads of stage s have landed (exact per-wave counts: the number of
+// loads a producer issues per stage varies with the item), one s_barrier for
+// all 12 waves, then producers refill the ring slots stage s - 1 used and
+// consumers compute stage s.
+//
+// Work split ("units"): an item is (tile of <= 64 rows of one expert, up to 8
+// consecutive weight units of 32 rows).  The XCD's tiles x units form one
+// flattened sequence; its Gx workgroups take equal contiguous ranges of it
+// (cut at tile ends and at 8 units), so every CU streams the same number of
+// weight bytes whatever N / 256 is (MLP2's 2880 rows are 11.25 blocks of 256).
+constexpr int kSK = 128;        // k per stage
+constexpr int kSCons = 8;       // consumer waves
+constexpr int kSThreads = 12 * 64;
+constexpr int kSDW = 5;         // weight ring stages
+constexpr int kSDA = 4;         // activation ring stages
+constexpr int kSUnits = 8;      // weight units (32 rows) per item, at most
+
+struct SWSlot {
+    uint4 w[16][64];        // column tile j of the item: its packed 1 KB block for the stage
+    uint4 sc[64];           // e8m0 of the stage: tile j, row n at byte 64 j + 4 n (4 k groups)
+    uint16_t bias[512];     // (item's last stage) biases of weight rows 32 f .. 32 (f + cnt) - 1
+    int32_t slot[64];       // (item's last stage, MLP2) token-order slot of tile row r
+};
+struct SASlot {
+    uint4 a[64 * 16];       // tile row r, 16-byte unit u (k 8u..8u+7) at r * 16 + (u ^ (r & 15))
+};
+struct SShared {
+    SWSlot w[kSDW];
+    SASlot a[kSDA];
+};
+
+// s_waitcnt vmcnt(n) for a run-time n (wave-uniform): the instruction takes
+// an immediate, so branch to it.
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+#define W4(b) case b: wait_vmcnt<b>(); break; case b + 1: wait_vmcnt<b + 1>(); break; \
+              case b + 2: wait_vmcnt<b + 2>(); break; case b + 3: wait_vmcnt<b + 3>(); break;
+    switch (n) {
+        W4(0) W4(4) W4(8) W4(12) W4(16) W4(20) W4(24) W4(28)
+        W4(32) W4(36) W4(40) W4(44) W4(48) W4(52) W4(56)
+        case 60: wait_vmcnt<60>(); break;
+        case 61: wait_vmcnt<61>(); break;
+        case 62: wait_vmcnt<62>(); break;
+        default: wait_vmcnt<63>(); break;
+    }
+#undef W4
+}
+
+// Barrier that keeps LDS accesses on their side of it and inserts no wait.
+__device__ __forceinline__ void s_barrier_mem() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ void lds_dma16_nt(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 2);  // nontemporal: streamed once
+}
+
+struct SArgs {
+    GemmArgs g;
+    const uint4 *pw;          // packed nibbles of this matrix
+    const uint8_t *ps;        // packed scales: [e][kp][ct][16 rows][4 B]
+    const int32_t *a_token;   // MLP1: tile row -> token (x row); MLP2: nullptr (act rows)
+};
+
+// Walks one workgroup's items stage by stage.  Items: the XCD's flattened
+// (tile, unit) range [u, u_end), cut at tile ends and at kSUnits units.
+struct SCursor {
+    int t, f, cnt, kp, left;  // tile index in the XCD list, first unit, units, stage, units left
+    int UPT, KP;
+    Tile tl;
+    const Tile *tiles;
+    int base;
+    __device__ __forceinline__ void load_tile() {
+        typedef const __attribute__((address_space(4))) int32_t *ConstInts;
+        const ConstInts p = (ConstInts)(tiles + base + t);
+        tl.expert = p[0];
+        tl.row0 = p[1];
+        tl.rows = p[2];
+        tl.pad = 0;
+    }
+    __device__ __forceinline__ void set_cnt() { cnt = min(kSUnits, min(UPT - f, left)); }
+    __device__ __forceinline__ void init(const Tile *tiles_, int base_, int ntx, int UPT_, int KP_,
+                                         int w, int Gx) {
+        tiles = tiles_;
+        base = base_;
+        UPT = UPT_;
+        KP = KP_;
+        const long total = (long)ntx * UPT;
+        const int u0 = (int)(total * w / Gx), u1 = (int)(total * (w + 1) / Gx);
+        left = u1 - u0;
+        t = UPT > 0 ? u0 / UPT : 0;
+        f = u0 - t * UPT;
+        kp = 0;
+        cnt = 0;
+        if (left > 0) {
+            load_tile();
+            set_cnt();
+        }
+    }
+    __device__ __forceinline__ bool valid() const { return left > 0; }
+    __device__ __forceinline__ void next() {
+        if (++kp < KP) return;
+        kp = 0;
+        left -= cnt;
+        f += cnt;
+        if (f == UPT) {
+            f = 0;
+            ++t;
+            if (left > 0) load_tile();
+        }
+        if (left > 0) set_cnt();
+    }
+};
+
+// One stage (NKS k steps of 32) of consumer c: weight unit c of the item
+// against MT 16-row groups of the tile.
+template <int MT, int NKS>
+__device__ __forceinline__ void s_compute(const SWSlot &ws, const SASlot &as, int c,
+                                          f32x4 (&acc)[4][2]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    u32x4 wv[2];
+    uint32_t sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        wv[t] = *reinterpret_cast<const u32x4 *>(&ws.w[2 * c + t][lane]);
+        sc[t] = reinterpret_cast<const uint32_t *>(ws.sc)[(2 * c + t) * 16 + n];
+    }
+    const char *arow = reinterpret_cast<const char *>(as.a) + n * 256;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        bf16x8 b[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t e = (sc[t] >> (8 * ks)) & 0xffu;
+            // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
+            const uint32_t q = wv[t][ks] & (e == 0 ? 0x88888888u : 0xffffffffu);
+            b[t] = dequant8(q, e8m0_to_f32(e));
+        }
+        const int uo = ((4 * ks + g) ^ n) * 16;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(arow + m * 4096 + uo));
+            acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[0], acc[m][0], 0, 0, 0);
+            acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[1], acc[m][1], 0, 0, 0);
+        }
+    }
+}
+
+template <int MT, bool kMlp1>
+__device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlot &ws, const Tile &tl,
+                                           int f, int c, const f32x4 (&acc)[4][2]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int N = a.N;
+    if (kMlp1) {
+        const int D = N / 2;
+        const int jc = 16 * (f + c) + n;  // output column: gate row 2 jc, up row 2 jc + 1
+        const uint32_t gu = reinterpret_cast<const uint32_t *>(ws.bias)[16 * c + n];
+        const float bg = __uint_as_float(gu << 16);
+        const float bu = __uint_as_float(gu & 0xffff0000u);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * m + 4 * g + v;
+                if (r < tl.rows) {
+                    float gt = bf16_round(acc[m][0][v] + bg);
+                    float up = bf16_round(acc[m][1][v] + bu);
+                    gt = fminf(fmaxf(gt, -a.limit), a.limit);
+                    up = fminf(fmaxf(up, -a.limit), a.limit);
+                    const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
+                    gt = gt * sig;
+                    a.out_act[(size_t)(tl.row0 + r) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                }
+            }
+    } else {
+        const int h = 32 * (f + c) + n;
+        const float b0 = bf2f(ws.bias[32 * c + n]), b1 = bf2f(ws.bias[32 * c + 16 + n]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * m + 4 * g + v;
+                if (r < tl.rows) {
+                    uint16_t *dst = a.out_slots + (size_t)ws.slot[r] * N + h;
+                    dst[0] = f2bf(acc[m][0][v] + b0);
+                    dst[16] = f2bf(acc[m][1][v] + b1);
+                }
+            }
+    }
+}
+
+template <bool kMlp1>
+__global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
+    __shared__ SShared sh;
+    const GemmArgs &a = d.g;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int N = a.N, K = a.K;
+    const int CT = N / 16, UPT = N / 32, KP = (K + kSK - 1) / kSK;
+    const int xcd = (int)blockIdx.x & 7, wg = (int)blockIdx.x >> 3, Gx = (int)gridDim.x >> 3;
+    typedef const __attribute__((address_space(4))) int32_t *ConstInts;
+    const int base = ((ConstInts)a.hdr)[HDR_XSTART + xcd];
+    const int ntx = ((ConstInts)a.hdr)[HDR_XCOUNT + xcd];
+    SCursor cur;
+    cur.init(a.tiles, base, ntx, UPT, KP, wg, Gx);
+    if (!cur.valid()) return;
+
+    if (wave < kSCons) {
+        // ------------------------------------------------ consumers
+        f32x4 acc[4][2];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const bool half_k = (K % kSK) != 0;  // the last stage holds 64 k
+        for (int s = 0; cur.valid(); ++s, cur.next()) {
+            s_barrier_mem();
+            const SWSlot &ws = sh.w[s % kSDW];
+            const SASlot &as = sh.a[s % kSDA];
+            const int mt = (cur.tl.rows + 15) >> 4;
+            const bool last = cur.kp == KP - 1;
+            if (wave < cur.cnt) {
+                if (last && half_k) {
+                    if (mt <= 1) s_compute<1, 2>(ws, as, wave, acc);
+                    else if (mt == 2) s_compute<2, 2>(ws, as, wave, acc);
+                    else if (mt == 3) s_compute<3, 2>(ws, as, wave, acc);
+                    else s_compute<4, 2>(ws, as, wave, acc);
+                } else {
+                    if (mt <= 1) s_compute<1, 4>(ws, as, wave, acc);
+                    else if (mt == 2) s_compute<2, 4>(ws, as, wave, acc);
+                    else if (mt == 3) s_compute<3, 4>(ws, as, wave, acc);
+                    else s_compute<4, 4>(ws, as, wave, acc);
+                }
+                if (last) {
+                    if (mt <= 1) s_epilogue<1, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
+                    else if (mt == 2) s_epilogue<2, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
+                    else if (mt == 3) s_epilogue<3, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
+                    else s_epilogue<4, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+        return;
+    }
+
+    // ---------------------------------------------------- producers
+    // Per-lane byte offsets are computed once per item, so a load is an SGPR
+    // base plus a VGPR offset: the producers spend their issue slots on the
+    // loads themselves.  Each producer counts its own loads exactly: ring
+    // byte st % 8 = the loads it issued for stage st (at most depth - 1
+    // stages are outstanding).
+    const bool wprod = wave < kSCons + 2;
+    const int p = wprod ? wave - kSCons : wave - kSCons - 2;  // 0 / 1
+    const int depth = wprod ? kSDW : kSDA;
+    uint64_t ring = 0;
+    int issued = 0, done = 0, is = 0;
+    SCursor icur = cur;  // issue cursor
+    const uint32_t lane16 = 16u * (uint32_t)lane;
+    uint32_t aoff[8];    // activation producers: byte offset of load i's 16 bytes (from A)
+    int ng = 0;          // activation producers: 16-row groups this wave loads for the item
+    uint32_t soff = 0;   // weight producer 0: byte offset of this lane's scales (from the stage's row)
+    const char *Ab = reinterpret_cast<const char *>(a.A);
+    const char *Wb = reinterpret_cast<const char *>(d.pw);
+
+    auto item_setup = [&](const SCursor &c) {
+        const Tile &tl = c.tl;
+        if (wprod) {
+            soff = (uint32_t)(min(lane >> 2, 2 * c.cnt - 1) * 64 + 16 * (lane & 3));
+            return;
+        }
+        const int mt = (tl.rows + 15) >> 4;
+        ng = min(max(mt - 2 * p, 0), 2);
+        if (ng == 0) return;
+        const int rlim = tl.rows - 1 - 32 * p;  // last valid row of this wave's 32, relative
+        const int q = lane >> 4;
+        int rowv = 0;  // lane j < 32: activation row of item row 32 p + j (unclamped)
+        if (d.a_token != nullptr) {
+            // the 32 tokens as scalars, spread over lanes 0..31
+            const ConstInts rt = (ConstInts)(d.a_token + tl.row0 + 32 * p);
+            int tk[32];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) tk[j] = rt[j];
+#pragma unroll
+            for (int j = 0; j < 32; ++j)
+                asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(rowv) : "s"(tk[j]), "n"(j));
+        } else {
+            rowv = tl.row0 + 32 * p + (lane & 31);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int rel = min(4 * i + q, rlim);              // clamped row within the 32
+            const int row = __shfl(rowv, rel);
+            const int u = (lane & 15) ^ ((4 * i + q) & 15);   // the LDS position's k unit
+            aoff[i] = (uint32_t)row * (uint32_t)(2 * K) + 16u * (uint32_t)u;
+        }
+    };
+
+    auto issue = [&](int st, const SCursor &c) {
+        int n_ld = 0;
+        const Tile &tl = c.tl;
+        if (c.kp == 0) item_setup(c);
+        if (wprod) {
+            SWSlot &ws = sh.w[st % kSDW];
+            const int ntile = 2 * c.cnt;
+            const int j1 = min(8 * p + 8, ntile);
+            // tile j's block for this stage: ((e CT + 2 f + j) KP + kp) KB
+            const char *wb = Wb + ((((size_t)tl.expert * CT + 2 * c.f + 8 * p) * KP + c.kp) << 10);
+            for (int j = 8 * p; j < j1; ++j) {
+                lds_dma16_nt(wb + lane16, &ws.w[j][0]);
+                wb += (size_t)KP << 10;
+                ++n_ld;
+            }
+            if (p == 0) {
+                const char *sb = reinterpret_cast<const char *>(d.ps) +
+                                 (((size_t)tl.expert * KP + c.kp) * CT + 2 * c.f) * 64;
+                lds_dma16_nt(sb + soff, &ws.sc[0]);
+                ++n_ld;
+            } else if (c.kp == KP - 1) {
+                // biases of rows 32 f .. 32 (f + cnt) - 1 (8 per lane)
+                const char *bb = reinterpret_cast<const char *>(a.bias + (size_t)tl.expert * N + 32 * c.f);
+                lds_dma16(bb + 16u * (uint32_t)min(lane, 4 * c.cnt - 1), &ws.bias[0]);
+                ++n_ld;
+                if (!kMlp1) {
+                    const char *rs = reinterpret_cast<const char *>(a.row_slot + tl.row0);
+                    lds_dma4(rs + 4u * (uint32_t)min(lane, tl.rows - 1), &ws.slot[0]);
+                    ++n_ld;
+                }
+            }
+        } else if (ng > 0) {
+            SASlot &as = sh.a[st % kSDA];
+            const char *ab = Ab + (size_t)c.kp * (2 * kSK);
+            const bool half = c.kp * kSK + kSK > K;  // only k units 0..7 exist
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (i < 4 * ng) {
+                    uint32_t o = aoff[i];
+                    // past K: reread unit u - 8 of the row (in bounds; never computed on)
+                    if (half && ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)) >= 8) o -= 128u;
+                    lds_dma16(ab + o, &as.a[(32 * p + 4 * i) * 16]);
+                    ++n_ld;
+                }
+            }
+        }
+        ring = (ring & ~(0xffull << (8 * (st & 7)))) | ((uint64_t)n_ld << (8 * (st & 7)));
+        issued += n_ld;
+    };
+
+    for (; is < depth - 1 && icur.valid(); ++is, icur.next()) issue(is, icur);
+    for (int s = 0; s < is; ++s) {
+        done += (int)((ring >> (8 * (s & 7))) & 0xff);
+        wait_vmcnt_dyn(issued - done);  // this wave's loads of stage s have landed
+        s_barrier_mem();
+        if (icur.valid()) {
+            issue(is, icur);
+            ++is;
+            icur.next();
+        }
+    }
+    wait_vmcnt<0>();
+}
+
 // fp32 -> MXFP4 (quantize_pack_mxfp4_block32_kernel, mxfp4.hpp:112-217), the
 // load-time quantiser of the reference's weight loader.  One 32-lane half of
 // a wave per 32-element block of the flattened array (tail zero-filled):
@@ -2784,10 +3152,9 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         hipLaunchKernelGGL(large_m_gemm_kernel<true>, dim3(cap), dim3(kLWaves * 64), 0, st, a1,
                            p.counts, p.offsets, s->n_experts);
     else if (direct)
-        hipLaunchKernelGGL((direct_gemm_kernel<true, 0>), dim3(cap), dim3(kDWaves * 64), 0, st,
-                           DArgs{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
-                                 reinterpret_cast<const uint4 *>(w->packed + PL.s1), p.row_token,
-                                 nullptr});
+        hipLaunchKernelGGL(stream_gemm_kernel<true>, dim3(cap), dim3(kSThreads), 0, st,
+                           SArgs{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
+                                 w->packed + PL.s1, p.row_token});
     else if (fp4) {
         launch_quantize_act(x, T, H, terms, nullptr, p.xq, p.xqs, st);
         GemmArgs aq1 = a1;
@@ -2816,9 +3183,9 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         hipLaunchKernelGGL(large_m_gemm_kernel<false>, dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                            p.counts, p.offsets, s->n_experts);
     else if (direct)
-        hipLaunchKernelGGL((direct_gemm_kernel<false, 0>), dim3(cap), dim3(kDWaves * 64), 0, st,
-                           DArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
-                                 reinterpret_cast<const uint4 *>(w->packed + PL.s2), nullptr, nullptr});
+        hipLaunchKernelGGL(stream_gemm_kernel<false>, dim3(cap), dim3(kSThreads), 0, st,
+                           SArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
+                                 w->packed + PL.s2, nullptr});
     else if (fp4) {
         // rows past offsets[E] (the live rows) are skipped
         launch_quantize_act(p.act, T * s->top_k, D, terms, p.offsets + s->n_experts, p.aq, p.aqs, st);

@@ -1,0 +1,190 @@
+"""CPU checks of the streamed expert GEMM's (stream_gemm_kernel) work split
+and load addresses.  The index arithmetic below restates the kernel's
+(SCursor, item_setup, issue) with numpy over lanes, so that a load outside
+its buffer, an LDS write outside its slot, or a (tile, unit) pair computed
+twice or never is caught without a GPU."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gptoss_moe as gm
+
+SK = 128          # k per stage
+UNITS = 8         # weight units (32 rows) per item, at most
+LANE = np.arange(64)
+
+
+def cursor_items(ntx, UPT, w, Gx):
+    """SCursor.init / next(): the items (tile, first unit, units) of workgroup
+    w of Gx on an XCD holding ntx tiles of UPT units each."""
+    total = ntx * UPT
+    u0, u1 = total * w // Gx, total * (w + 1) // Gx
+    left = u1 - u0
+    t = u0 // UPT if UPT else 0
+    f = u0 - t * UPT
+    items = []
+    while left > 0:
+        cnt = min(UNITS, UPT - f, left)
+        items.append((t, f, cnt))
+        left -= cnt
+        f += cnt
+        if f == UPT:
+            f, t = 0, t + 1
+    return items
+
+
+@pytest.mark.parametrize("ntx,UPT,Gx", [(4, 180, 32), (4, 90, 32), (16, 180, 32), (1, 4, 32),
+                                        (0, 90, 32), (3, 8, 32), (33, 90, 32), (5, 7, 3),
+                                        (32, 180, 32), (2, 2, 32)])
+def test_items_cover_every_tile_unit_once(ntx, UPT, Gx):
+    seen = np.zeros((ntx, UPT), np.int64)
+    per_wg = []
+    for w in range(Gx):
+        its = cursor_items(ntx, UPT, w, Gx)
+        per_wg.append(sum(c for _, _, c in its))
+        for t, f, c in its:
+            assert 1 <= c <= UNITS
+            assert 0 <= t < ntx and 0 <= f and f + c <= UPT  # an item stays inside its tile
+            seen[t, f:f + c] += 1
+    assert (seen == 1).all()
+    # every workgroup streams the same number of weight units, within one
+    assert max(per_wg) - min(per_wg) <= 1
+
+
+def weight_dma(E, N, K, e, f, cnt, kp):
+    """issue(), weight producers: byte offsets (within the matrix's packed
+    nibbles) of the 16 bytes each lane loads for every column tile j of the
+    item, and the LDS tile index j."""
+    CT, KP = N // 16, -(-K // 128)
+    offs = []
+    for j in range(2 * cnt):
+        blk = ((e * CT + 2 * f + j) * KP + kp)
+        offs.append(blk * 1024 + 16 * LANE)
+    return np.concatenate(offs), 2 * cnt
+
+
+def scale_dma(E, N, K, e, f, cnt, kp):
+    """Weight producer 0: one 16-byte load per lane of the item's e8m0 block
+    ([e][kp][ct][16 rows][4 B]); lane l covers tile min(l / 4, 2 cnt - 1)."""
+    CT, KP = N // 16, -(-K // 128)
+    jt = np.minimum(LANE >> 2, 2 * cnt - 1)
+    return (((e * KP + kp) * CT + 2 * f + jt) * 64 + 16 * (LANE & 3))
+
+
+@pytest.mark.parametrize("N,K", [(5760, 2880), (2880, 2880), (256, 128), (128, 128), (192, 448),
+                                 (896, 192), (6144, 3072), (64, 3072), (128, 64)])
+def test_weight_scale_bias_loads_in_bounds(N, K):
+    E = 3
+    CT, KP, KQ, UPT = N // 16, -(-K // 128), -(-K // 512), N // 32
+    nib_bytes = E * N * KP * 64                # packed nibbles of one matrix
+    sc_bytes = E * N * KQ * 16                 # its scale region (sized for the FP4 layout)
+    assert E * KP * CT * 64 <= sc_bytes        # the streamed layout fits the region
+    for e in (0, E - 1):
+        for f in range(0, UPT):
+            for cnt in range(1, min(UNITS, UPT - f) + 1):
+                for kp in (0, KP - 1):
+                    o, ntile = weight_dma(E, N, K, e, f, cnt, kp)
+                    assert o.min() >= 0 and o.max() + 16 <= nib_bytes and ntile <= 16
+                    s = scale_dma(E, N, K, e, f, cnt, kp)
+                    assert s.min() >= 0 and s.max() + 16 <= sc_bytes
+                    # the scales of the item's tiles are the ones the lanes read
+                    ct = 2 * f + (LANE >> 2)
+                    ok = (LANE >> 2) < 2 * cnt
+                    want = ((e * KP + kp) * CT + ct) * 64 + 16 * (LANE & 3)
+                    assert np.array_equal(s[ok], want[ok])
+                # biases: 8 bf16 per lane from row 32 f + 8 min(l, 4 cnt - 1), inside the expert
+                l = np.minimum(LANE, 4 * cnt - 1)
+                first = e * N + 32 * f + 8 * l
+                assert first.min() >= e * N and (first + 8).max() <= (e + 1) * N
+                # lanes below 4 cnt cover rows 32 f .. 32 (f + cnt) - 1 exactly once
+                assert np.array_equal(np.sort(first[:4 * cnt]) - e * N, 32 * f + 8 * np.arange(4 * cnt))
+
+
+def act_dma(rows, K, kp, p, row0, token=None):
+    """item_setup + issue(), activation producer p: for each of its loads i,
+    the source element offset of every lane (from A) and the LDS unit it
+    fills; rows past the tile repeat its last row, and in a 64-k stage
+    (K % 128 == 64, last kp) units 8..15 reread units 0..7."""
+    mt = (rows + 15) >> 4
+    ng = min(max(mt - 2 * p, 0), 2)
+    rlim = rows - 1 - 32 * p
+    q = LANE >> 4
+    half = kp * SK + SK > K
+    out = []
+    for i in range(4 * ng):
+        rel = np.minimum(4 * i + q, rlim)
+        r_item = 32 * p + rel                    # clamped tile row
+        row = token[row0 + r_item] if token is not None else row0 + r_item
+        u = (LANE & 15) ^ ((4 * i + q) & 15)
+        o = row * (2 * K) + 16 * u + kp * 2 * SK
+        if half:
+            o = np.where(u >= 8, o - 128, o)
+        lds_unit = (32 * p + 4 * i) * 16 + LANE
+        out.append((o, lds_unit, r_item, u))
+    return out
+
+
+@pytest.mark.parametrize("K", [64, 128, 448, 2880, 3072])
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 32, 33, 48, 63, 64])
+def test_activation_loads(K, rows):
+    """Every activation load stays inside its source row (bytes of row `row`
+    only), every LDS unit of the row groups the MFMAs read is written exactly
+    once per stage, and the unit at LDS position r * 16 + (U ^ (r & 15))
+    holds row r's k unit U (the consumer's read form)."""
+    KP = -(-K // SK)
+    T = 300
+    rng = np.random.default_rng(rows * 7 + K)
+    token = rng.integers(0, T, size=400)
+    row0 = 5
+    mt = (rows + 15) >> 4
+    for kp in range(KP):
+        written = np.full(64 * 16, -1, np.int64)
+        for p in (0, 1):
+            for tok in (None, token):
+                for o, unit, r_item, u in act_dma(rows, K, kp, p, row0, tok):
+                    src_row = tok[row0 + r_item] if tok is not None else row0 + r_item
+                    assert (o >= src_row * 2 * K).all() and (o + 16 <= (src_row + 1) * 2 * K).all()
+                    assert (o % 16 == 0).all()
+                    if tok is None:
+                        written[unit] = o
+                    assert unit.max() < 64 * 16
+        # coverage of the MFMA row groups
+        need = 16 * mt
+        assert (written[:need * 16] >= 0).all()
+        # consumer read form: row r, k unit U at LDS unit r * 16 + (U ^ (r & 15))
+        nks = 2 if kp * SK + SK > K else 4
+        for r in range(need):
+            rc = min(r, rows - 1)
+            for U in range(4 * nks):  # only the k steps the consumers compute
+                got = written[r * 16 + (U ^ (r & 15))]
+                assert got == (row0 + rc) * 2 * K + kp * 2 * SK + 16 * U
+
+
+def test_token_scalar_reads_stay_in_workspace():
+    """item_setup reads 32 row tokens per activation producer without
+    clamping (rows past the tile are never used): the furthest index,
+    row0 + 63 with row0 + rows <= P, must stay inside the workspace."""
+    lib = gm.load_library()
+    for H, D, E, k, T in ((2880, 2880, 32, 4, 256), (128, 128, 4, 2, 1), (128, 128, 4, 1, 1),
+                          (2880, 2880, 128, 4, 1), (256, 256, 8, 8, 3)):
+        s = gm.make_shape(H, D, E, k)
+        size = gm.workspace_size(s, T)
+        base = 1 << 20
+        v = gm.Views()
+        assert lib.gptoss_moe_workspace_views(ctypes.byref(s), T, ctypes.c_void_p(base), size,
+                                              ctypes.byref(v)) == 0
+        P = T * k
+        rt_off = v.row_token - base
+        furthest = rt_off + 4 * (P - 1 + 63) + 4
+        assert furthest <= size, (H, D, E, k, T)
+        # and never into the activations the same call writes
+        assert furthest <= v.act - base
+
+
+def test_lds_layout_fits():
+    """Weight ring 5 x (16 tiles x 1 KB + 1 KB scales + 1 KB biases + 256 B
+    slots) + activation ring 4 x 16 KB fits gfx950's 160 KB."""
+    wslot = 16 * 1024 + 1024 + 1024 + 256
+    aslot = 64 * 256
+    assert 5 * wslot + 4 * aslot <= 160 * 1024
