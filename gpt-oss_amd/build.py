@@ -20,8 +20,13 @@ SOURCES = [os.path.join(HERE, "csrc", "gptoss_moe.hip"), os.path.join(HERE, "csr
 LIB = os.path.join(HERE, "libgptoss_moe.so")
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *HIP_FLAGS, *SOURCES, "-o", LIB]
+# A C++ caller of the library and of the moe_gpu shim (csrc/moe_gpu_shim.hpp),
+# run by tests/test_gpu_cpp_shim.py; links the in-tree library by rpath.
+SHIM_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "moe_gpu_test.cpp")
+SHIM_TEST_BIN = os.path.join(HERE, "bin", "moe_gpu_test")
+
+
+def _run(cmd, verbose):
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                      if "packed-fp32-ops" not in l)
@@ -29,6 +34,16 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{msgs}")
     if verbose and msgs.strip():
         print(msgs)
+
+
+def build(verbose: bool = False) -> str:
+    _run([HIPCC, *HIP_FLAGS, *SOURCES, "-o", LIB], verbose)
+    os.makedirs(os.path.dirname(SHIM_TEST_BIN), exist_ok=True)
+    _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
+          "-x", "hip", SHIM_TEST_SRC, "-L", HERE, "-lgptoss_moe",
+          "-Wl,-rpath,$ORIGIN/..", "-o", SHIM_TEST_BIN], verbose)
     return LIB
 
 

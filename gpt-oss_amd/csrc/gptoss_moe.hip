@@ -636,6 +636,11 @@ __device__ __forceinline__ void expert_offsets(const int *tot, int *offs, int E,
     if (lane == 63) offs[E] = off;
 }
 
+// Workgroups of an index_kernel grid (G, n_blk + 1) that reach its
+// histogram-clearing counter: all but the planners (g > 0, n_blk), which
+// return before doing anything.
+__host__ __device__ constexpr int index_arrivals(int G, int n_blk) { return G * n_blk + 1; }
+
 // Plan, compact row map and gather in one launch (route_build_index_kernel_bf16wts,
 // moe.hpp:1173-1270, and pack_rows_kernel_bf16_in, moe.hpp:983-1048).
 // Grid (G, n_blk + 1).  Every workgroup of rows b < n_blk:
@@ -790,11 +795,15 @@ __global__ __launch_bounds__(256) void index_kernel(
         }
         lds_barrier();
     }
-    // the last workgroup to finish (all histogram reads have returned by
-    // now: their values were used above) clears the histogram
+    // The last workgroup to finish clears the histogram.  Every workgroup
+    // reaching this point has used the histogram values it loaded (the plan
+    // stage above consumed them), so none of its reads is still in flight.
+    // Arrivals: the G x n_blk row workgroups and the planner (0, n_blk); the
+    // planners (g > 0, n_blk) returned at the start and never arrive.
+    const int arrivals = index_arrivals(G, n_blk);
     if (tid == 0)
         last = __hip_atomic_fetch_add(&hdr[HDR_DONE], 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == G * n_blk;
+                                      __HIP_MEMORY_SCOPE_AGENT) == arrivals - 1;
     lds_barrier();
     if (last) {
         for (int i = tid; i < n_blk * kHistCols; i += 256) hist[i] = 0;
@@ -3096,11 +3105,21 @@ int gemm_tile_rows(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T
     return p == PATH_DIRECT || p == PATH_FP4 ? kDTileRows : kTileRows;
 }
 
-// Expert weights and flags of a forward call.
+// Expert weights and flags of a forward call.  The streamed GEMM (packed set,
+// no SMALL_M / LARGE_M flag) and the FP4 variant (packed_fp4) read only their
+// packed copy and the biases, so w1 / w2 and their scales may then be NULL
+// (the caller may free them after packing).
 int check_experts(const gptoss_moe_weights *w, unsigned flags) {
     if (flags & ~kFlagsAll) return GPTOSS_MOE_ERR_INVALID_ARG;
-    if (!w->w1 || !w->w1_scales || !w->b1 || !w->w2 || !w->w2_scales || !w->b2)
+    if (!w->b1 || !w->b2) return GPTOSS_MOE_ERR_INVALID_ARG;
+    const bool fp4 = (flags & GPTOSS_MOE_FLAG_FP4_MFMA) != 0;
+    const bool packed_only =
+        fp4 ? w->packed_fp4 != nullptr
+            : (w->packed != nullptr &&
+               !(flags & (GPTOSS_MOE_FLAG_SMALL_M_GEMM | GPTOSS_MOE_FLAG_LARGE_M_GEMM)));
+    if (!packed_only && (!w->w1 || !w->w1_scales || !w->w2 || !w->w2_scales))
         return GPTOSS_MOE_ERR_INVALID_ARG;
+    if (!aligned16(w->b1) || !aligned16(w->b2)) return GPTOSS_MOE_ERR_INVALID_ARG;
     if (!aligned16(w->w1) || !aligned16(w->w2) || !aligned16(w->packed) || !aligned16(w->packed_fp4))
         return GPTOSS_MOE_ERR_INVALID_ARG;
     if ((flags & GPTOSS_MOE_FLAG_FP4_MFMA) && w->packed_fp4 == nullptr) return GPTOSS_MOE_ERR_INVALID_ARG;
@@ -3367,7 +3386,10 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
     Marks mk;
     mk.on = true;
     for (int i = 0; i < 6; ++i)
-        if ((rc = hip_status(hipEventCreate(&mk.ev[i]))) != 0) return rc;
+        if ((rc = hip_status(hipEventCreate(&mk.ev[i]))) != 0) {
+            for (int j = 0; j < i; ++j) (void)hipEventDestroy(mk.ev[j]);
+            return rc;
+        }
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
     mk.mark(stream);
@@ -3399,6 +3421,13 @@ int gptoss_moe_layer(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
     if ((rc = check_experts(w, 0)) != 0) return rc;
     if (n_tokens == 0) return GPTOSS_MOE_OK;
     if (!aligned16(x) || !aligned16(t_scratch)) return GPTOSS_MOE_ERR_INVALID_ARG;
+    {
+        // t_scratch receives RMSNorm(x) before the residual add reads x: the
+        // two ranges must not overlap
+        const uintptr_t xb = (uintptr_t)x, tb = (uintptr_t)t_scratch;
+        const uintptr_t len = (uintptr_t)n_tokens * (uintptr_t)shape->hidden * 2u;
+        if (xb < tb + len && tb < xb + len) return GPTOSS_MOE_ERR_INVALID_ARG;
+    }
     // RMSNorm fused into the router kernel (t_scratch = RMSNorm(x)), the GEMMs
     // on t_scratch, the residual add in the finalize kernel
     const WsLayout L = ws_layout(*shape, max_tokens);

@@ -236,6 +236,17 @@ class MoeLayer:
         self.tensors.pop("packed", None)
         self.w.packed = None
 
+    def drop_unpacked(self):
+        """Free w1/w2 and their scales once the packed copy exists: the
+        streamed GEMM reads only `packed` and the biases (include/gptoss_moe.h),
+        so the layer then holds one copy of its expert weights.  Forcing an
+        LDS-staged path afterwards is rejected by the library."""
+        if self.w.packed is None:
+            raise MoeError("drop_unpacked", ERR_INVALID_ARG)
+        for n in ("w1", "w1_scales", "w2", "w2_scales"):
+            self.tensors.pop(n, None)
+            setattr(self.w, n, None)
+
     @classmethod
     def from_numpy(cls, d, max_tokens: Optional[int] = None, device="cuda",
                    pack: bool = True, pack_fp4: bool = False) -> "MoeLayer":
@@ -265,8 +276,16 @@ class MoeLayer:
         import torch
         lib = load_library()
         cfg = read_bin_config(path)
-        dev = torch.device(device)
         H, D, E = cfg.hidden_dim, cfg.intermediate_dim, cfg.n_experts
+        # the header must describe a layer this library runs and a file of
+        # exactly the size it implies, before any device buffer is sized from it
+        if H <= 0 or D <= 0 or H % 64 or D % 64 or not 1 <= E <= 256 or \
+                not 1 <= cfg.experts_per_token <= min(8, E):
+            raise MoeError("gptoss_moe_bin_read_config", ERR_UNSUPPORTED)
+        offs = bin_layer_offsets(cfg, layer)
+        if offs.file_bytes != os.path.getsize(path):
+            raise MoeError("gptoss_moe_bin_layer_offsets", ERR_INVALID_ARG)
+        dev = torch.device(device)
         u8 = lambda n: torch.empty(n, dtype=torch.uint8, device=dev)
         i16 = lambda n: torch.empty(n, dtype=torch.int16, device=dev)
         w = {"w1": u8(E * 2 * D * H // 2), "w1_scales": u8(E * 2 * D * H // 32),

@@ -72,7 +72,12 @@ typedef struct gptoss_moe_shape {
 } gptoss_moe_shape;
 
 /* One layer's MoE weights (GPUTransformerWeights MoE fields,
- * getp_run.cpp:65-77, at one layer offset).  All device pointers. */
+ * getp_run.cpp:65-77, at one layer offset).  All device pointers; w1, w2,
+ * packed, packed_fp4, b1 and b2 16-byte aligned.  When `packed` is set (and
+ * no SMALL_M / LARGE_M flag is passed), or for FP4_MFMA when `packed_fp4` is
+ * set, the forward reads only that packed copy and the biases: w1, w2 and
+ * their scales may then be NULL, so a caller can free them after packing
+ * and keep one copy of the weights. */
 typedef struct gptoss_moe_weights {
     const uint16_t *router_w;  /* bf16 [E][H] (w_router, used as out x in) */
     const uint16_t *router_b;  /* bf16 [E] */

@@ -123,3 +123,58 @@ def test_noalloc_rejects_without_gpu_work():
                                           None, None, 0, None) == gm.ERR_WORKSPACE
     assert lib.gptoss_moe_forward_noalloc(ctypes.byref(s20), ctypes.byref(w), None, None, -1,
                                           None, None, 0, None) == gm.ERR_INVALID_ARG
+
+
+def _fake_call(lib, shape, w, flags=0, n_tokens=0):
+    """gptoss_moe_forward on zero tokens: every argument is validated, no GPU
+    work is issued (the workspace pointer is never dereferenced)."""
+    ws_bytes = gm.workspace_size(shape, 16)
+    fake = ctypes.c_void_p(1 << 30)
+    return lib.gptoss_moe_forward(ctypes.byref(shape), ctypes.byref(w), fake, fake, n_tokens, None,
+                                  None, flags, fake, ws_bytes, 16, None)
+
+
+def test_packed_weights_make_w1_w2_optional():
+    lib = gm.load_library()
+    s = gm.make_shape(2880, 2880, 32, 4)
+    p = 1 << 20  # aligned stand-in device addresses
+    base = dict(router_w=p, router_b=p, b1=p, b2=p)
+    # packed copy only: the streamed GEMM needs nothing else
+    w = gm.Weights(**base, packed=p)
+    assert _fake_call(lib, s, w) == gm.OK
+    # no packed copy and no w1/w2: nothing to run on
+    w = gm.Weights(**base)
+    assert _fake_call(lib, s, w) == gm.ERR_INVALID_ARG
+    # a forced LDS-staged path reads w1/w2 even with a packed copy
+    w = gm.Weights(**base, packed=p)
+    assert _fake_call(lib, s, w, gm.FLAG_SMALL_M_GEMM) == gm.ERR_INVALID_ARG
+    assert _fake_call(lib, s, w, gm.FLAG_LARGE_M_GEMM) == gm.ERR_INVALID_ARG
+    # the FP4 variant needs packed_fp4, not w1/w2
+    w = gm.Weights(**base, packed_fp4=p)
+    assert _fake_call(lib, s, w, gm.FLAG_FP4_MFMA) == gm.OK
+    w = gm.Weights(**base, packed=p)
+    assert _fake_call(lib, s, w, gm.FLAG_FP4_MFMA) == gm.ERR_INVALID_ARG
+    # biases are always read
+    w = gm.Weights(router_w=p, router_b=p, b2=p, packed=p)
+    assert _fake_call(lib, s, w) == gm.ERR_INVALID_ARG
+    # misaligned bias (16-byte loads)
+    w = gm.Weights(**{**base, "b1": p + 2}, packed=p)
+    assert _fake_call(lib, s, w) == gm.ERR_INVALID_ARG
+
+
+def test_layer_rejects_overlapping_x_and_t_scratch():
+    """gptoss_moe_layer writes RMSNorm(x) into t_scratch before the residual
+    add reads x, so overlapping buffers are an argument error (checked before
+    any GPU work)."""
+    lib = gm.load_library()
+    s = gm.make_shape(128, 128, 4, 2)
+    p = 1 << 20
+    w = gm.Weights(router_w=p, router_b=p, b1=p, b2=p, packed=p)
+    T = 8
+    ws_bytes = gm.workspace_size(s, T)
+    ws = ctypes.c_void_p(1 << 30)
+    x = 1 << 28
+    for t in (x, x + 256, x - 256, x + T * 128 * 2 - 16):
+        rc = lib.gptoss_moe_layer(ctypes.byref(s), ctypes.byref(w), ctypes.c_void_p(p),
+                                  ctypes.c_void_p(x), ctypes.c_void_p(t), T, ws, ws_bytes, T, None)
+        assert rc == gm.ERR_INVALID_ARG, hex(t - x)

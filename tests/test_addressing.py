@@ -303,3 +303,32 @@ def test_items_cover_every_tile_block_once(ntx, nblk, Gx):
     # balanced: item counts per workgroup differ by at most one
     n = [len(got) for got in per_wg]
     assert max(n) - min(n) <= 1
+
+
+# ------------------------------------------------- index_kernel counter --
+def index_grid_arrivals(G, n_blk):
+    """index_kernel's grid (G, n_blk + 1): workgroup (g, b) returns at once
+    when it is a planner (b == n_blk) with g > 0; all others reach the
+    histogram-clearing counter."""
+    return [(g, b) for b in range(n_blk + 1) for g in range(G) if not (b == n_blk and g > 0)]
+
+
+@pytest.mark.parametrize("G,n_blk", [(1, 1), (1, 64), (2, 3), (64, 4), (256, 1), (8, 64)])
+def test_index_done_counter_clears_once_and_resets(G, n_blk):
+    """The done counter (hdr[HDR_DONE]) counts arrivals; the arrival that
+    reads index_arrivals(G, n_blk) - 1 = G * n_blk is the last, clears the
+    histogram and resets the counter to 0 for the next call, whatever grid
+    that call has."""
+    counter = 0
+    for grid in ((G, n_blk), (max(1, G // 2), n_blk + 1), (1, 1)):
+        arrivals = index_grid_arrivals(*grid)
+        expected = grid[0] * grid[1] + 1  # index_arrivals()
+        assert len(arrivals) == expected
+        lasts = 0
+        for _ in arrivals:  # any order: one fetch_add each
+            old = counter
+            counter += 1
+            if old == expected - 1:
+                lasts += 1
+                counter = 0  # the last workgroup resets it
+        assert lasts == 1 and counter == 0

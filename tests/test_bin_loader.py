@@ -65,3 +65,34 @@ def test_loader_argument_errors(tmp_path):
         assert rc == g.ERR_INVALID_ARG, (path, layer, nbytes, rc)
     cfg = g.BinConfig()
     assert lib.gptoss_moe_bin_read_config(b"/nonexistent.bin", ctypes.byref(cfg)) == g.ERR_INVALID_ARG
+
+
+def test_from_bin_checks_header_before_allocating(tmp_path, monkeypatch):
+    """MoeLayer.from_bin validates the header (supported shape) and the file
+    size it implies before it sizes any device buffer: a truncated file or
+    an unsupported shape raises MoeError, and torch.empty is never reached."""
+    g = _lib()
+    import torch
+
+    def no_alloc(*a, **k):
+        raise AssertionError("device allocation before the header was checked")
+    monkeypatch.setattr(torch, "empty", no_alloc)
+    c = dict(binfile.TINY)
+    p = str(tmp_path / "t.bin")
+    binfile.write_bin(p, c, lambda n, s: np.zeros(s, np.float32))
+    short = str(tmp_path / "short.bin")
+    with open(p, "rb") as f, open(short, "wb") as o:
+        o.write(f.read()[:-4])
+    with pytest.raises(g.MoeError) as e:
+        g.MoeLayer.from_bin(short, 0, max_tokens=4)
+    assert e.value.rc == g.ERR_INVALID_ARG
+    for bad in (dict(hidden_dim=100), dict(intermediate_dim=96), dict(experts_per_token=9),
+                dict(n_experts=0)):
+        cb = dict(c, **bad)
+        pb = str(tmp_path / "bad.bin")
+        try:
+            binfile.write_bin(pb, cb, lambda n, s: np.zeros(s, np.float32))
+        except ValueError:
+            continue
+        with pytest.raises(g.MoeError):
+            g.MoeLayer.from_bin(pb, 0, max_tokens=4)

@@ -1,0 +1,54 @@
+"""A C++ caller of the library (tests/cpp/moe_gpu_test.cpp, built by
+__graft_entry__.build()): gptoss_moe_forward from C++ against the committed
+golden fixture, and the moe_gpu shim (gpt-oss_amd/csrc/moe_gpu_shim.hpp,
+the reference's entry point and signature) on its 120B path (MXFP4 weight
+fields) and its 20B path (bf16 weight fields re-quantised at init) against
+the oracle's layer, on config c0."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+import synth
+from parity import assert_close
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "gpt-oss_amd", "bin", "moe_gpu_test")
+GOLDEN = os.path.join(ROOT, "tests", "golden", "c0_tiny.npz")
+
+
+def test_cpp_caller_and_moe_gpu_shim(tmp_path):
+    assert os.path.exists(BIN), "build it with __graft_entry__.build()"
+    d = synth.make_data("c0_tiny")
+    c = d.cfg
+    H, D, E, K, T = c.hidden, c.intermediate, c.n_experts, c.top_k, c.tokens
+    rms = synth.f32_to_bf16(1 + 0.1 * np.random.default_rng(9).standard_normal(H).astype(np.float32))
+    w1b = oracle.dequant(np.ascontiguousarray(d.w1).reshape(-1), np.ascontiguousarray(d.s1).reshape(-1),
+                         E * 2 * D * H)
+    w2b = oracle.dequant(np.ascontiguousarray(d.w2).reshape(-1), np.ascontiguousarray(d.s2).reshape(-1),
+                         E * H * D)
+    inp = tmp_path / "in.bin"
+    with open(inp, "wb") as f:
+        f.write(np.array([H, D, E, K, T], np.int32).tobytes())
+        for a in (d.x, rms, d.router_w, d.router_b, d.w1, d.s1, d.b1, d.w2, d.s2, d.b2, w1b, w2b):
+            f.write(np.ascontiguousarray(a).tobytes())
+    outp = tmp_path / "out.bin"
+    r = subprocess.run([BIN, str(inp), str(outp)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0
+    out = np.fromfile(outp, np.uint16).reshape(4, T, H)
+    e_agg, x_q, x_b, x_o = out
+    # the forward from C++ against the committed golden output
+    g = np.load(GOLDEN)
+    assert_close(e_agg, g["e_agg"], "gptoss_moe_forward from C++")
+    # the shim's layer against the oracle: x + MoE(RMSNorm(x))
+    t = oracle.rmsnorm(d.x, rms)
+    want = oracle.residual_add(d.x, oracle.moe_forward(d, x_norm=t, forced=False)["e_agg"])
+    assert_close(x_q, want, "moe_gpu, MXFP4 weight fields")
+    # re-quantising the bf16 weights reproduces the MXFP4 values: bit-identical layer
+    assert np.array_equal(x_b, x_q), "moe_gpu, bf16 weight fields"
+    # row_offset: rows before it untouched, rows from it as in the full call
+    assert np.array_equal(x_o[:3], d.x[:3]) and np.array_equal(x_o[3:], x_q[3:])
