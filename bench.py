@@ -82,13 +82,65 @@ def read_traffic(path: str, kernel: str):
     return int(round((row[0] * ff + row[1] * fw) * 1024))
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def parse_rocminfo(text: str, arch: str = "gfx950"):
+    """(compute units, max clock MHz) of the first `arch` agent in rocminfo's
+    output, or None."""
+    for block in text.split("*******"):
+        if not any(l.split(":", 1)[-1].strip() == arch for l in block.splitlines()
+                   if l.strip().startswith("Name:")):
+            continue
+        cu = mhz = None
+        for line in block.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip().split()
+            if not v:
+                continue
+            if k == "Compute Unit":
+                cu = int(v[0])
+            elif k.startswith("Max Clock Freq"):
+                mhz = int(v[0])
+        if cu and mhz:
+            return cu, mhz
+    return None
+
+
+def bf16_peak_tflops() -> dict:
+    """Dense bf16 MFMA peak of this GPU from rocminfo: CUs x max clock x 4096
+    FLOP per CU and clock (4 SIMDs x 512 bf16 FMAs); the published 2.5
+    PFLOP/s when rocminfo is unavailable."""
+    import subprocess
+    try:
+        r = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60)
+        got = parse_rocminfo(r.stdout)
+    except (OSError, subprocess.SubprocessError):
+        got = None
+    if got is None:
+        return {"tflops": BF16_PEAK_TFLOPS, "source": "published (rocminfo unavailable)"}
+    cu, mhz = got
+    return {"tflops": round(cu * mhz * 1e6 * 4096 / 1e12, 1), "compute_units": cu,
+            "max_clock_mhz": mhz, "source": "rocminfo: CUs x max clock x 4096 FLOP/clk"}
+
+
 def cpu_baseline(d, budget_s: float) -> dict:
     """The reference CPU engine's MoE block (run.cpp:657-748, OpenMP matmul)
-    restated in oracle/, one token at a time, on a bounded sample."""
+    restated in oracle/, one token at a time, on a bounded sample, built with
+    the reference's runomp flags (-O3 -fopenmp -march=native) for this host."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
     from synth import bf16_to_f32
+    native = oracle.use_native()
 
     eng = oracle.Fp32Engine(d)
     x = bf16_to_f32(d.x)
@@ -100,6 +152,9 @@ def cpu_baseline(d, budget_s: float) -> dict:
         n += 1
     dt = time.perf_counter() - t0
     return {"value": n / dt, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+            "cpu": cpu_model(), "logical_cpus": os.cpu_count(),
+            "build": "-O3 -fopenmp -march=native (built on this host)" if native
+                     else "-O3 -fopenmp -march=x86-64-v3 (native build failed)",
             "sample": f"{n} token evaluations cycling over the {d.cfg.tokens} tokens of "
                       f"{d.cfg.name}, one token at a time (run.cpp:657-748 restated, fp32 weights "
                       f"= exact MXFP4 dequant), {dt:.1f} s"}
@@ -271,17 +326,18 @@ def main():
     tok_s = c.tokens / (ms * 1e-3)
     traffic = read_traffic(args.traffic or os.path.join(ROOT, "profiles", f"hbm_traffic_{c.name}.txt"),
                            "mlp1")
+    peak = bf16_peak_tflops()
     if c.tokens * c.top_k >= 96 * c.n_experts:
         # prefill-sized: MLP1 is bound by the bf16 MFMA peak (2 D x H MACs per routed pair)
         mlp1_flops = 2 * pairs * (2 * D) * H
         tf = mlp1_flops / (kms["mlp1"] * 1e-3) / 1e12
-        roofline = {"bound": "mfma", "kernel": "direct_gemm_kernel<true> (MLP1)",
-                    "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+        roofline = {"bound": "mfma", "kernel": "stream_gemm_kernel<true> (MLP1)",
+                    "achieved": round(tf, 1), "peak": peak["tflops"], "unit": "TFLOP/s",
+                    "frac": round(tf / peak["tflops"], 4), "traffic": None,
                     "algorithmic_flops_per_launch": mlp1_flops,
-                    "avg_launch_ms": round(kms["mlp1"], 5)}
+                    "avg_launch_ms": round(kms["mlp1"], 5), "peak_source": peak}
     else:
-        roofline = {"bound": "hbm", "kernel": "direct_gemm_kernel<true> (MLP1)",
+        roofline = {"bound": "hbm", "kernel": "stream_gemm_kernel<true> (MLP1)",
                     "achieved": round(mlp1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(mlp1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                     "algorithmic_bytes_per_launch": mlp1_bytes,
@@ -308,7 +364,8 @@ def main():
         "layer": {"algorithmic_bytes": alg_bytes, "hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
                   "hbm_frac": round(alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                   "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-                  "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                  "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / peak["tflops"], 4),
+                  "bf16_peak_tflops": peak["tflops"],
                   "active_experts": active, "pairs": pairs},
         "kernel_ms": {k: round(v, 5) for k, v in kms.items()},
         "wall_s_timed": round(wall, 4),

@@ -128,6 +128,19 @@ def forced_routing(rng: np.random.Generator, scores: np.ndarray, K: int, kind: s
     return idx, f32_to_bf16(w.astype(np.float32))
 
 
+def make_router_inputs(cfg: MoeConfig | str):
+    """x, router weight and router bias of make_data(cfg), without the expert
+    weights (the same generator stream: these are drawn first)."""
+    if isinstance(cfg, str):
+        cfg = CONFIGS[cfg]
+    rng = np.random.Generator(np.random.PCG64(cfg.seed))
+    H, E, T = cfg.hidden, cfg.n_experts, cfg.tokens
+    x = _normal_bf16(rng, (T, H), 1.0)
+    wr = _normal_bf16(rng, (E, H), 0.02)
+    br = _normal_bf16(rng, (E,), 0.01)
+    return x, wr, br
+
+
 def make_data(cfg: MoeConfig | str, tokens: int | None = None) -> MoeData:
     if isinstance(cfg, str):
         cfg = CONFIGS[cfg]

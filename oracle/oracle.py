@@ -45,10 +45,25 @@ _SIGS = {
 }
 
 _lib = None
+NATIVE_PATH = os.path.join(_HERE, "_native", "liboracle_native.so")
 
 
 def build() -> None:
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def use_native() -> bool:
+    """Build the -march=native copy for this host (the reference's runomp
+    flags) and load it instead of the portable one; False if it cannot be
+    built here.  Call before any other oracle function."""
+    global LIB_PATH
+    if _lib is not None:
+        raise RuntimeError("oracle library already loaded")
+    r = subprocess.run(["make", "-s", "-B", "-C", _HERE, "native"], capture_output=True, text=True)
+    if r.returncode != 0 or not os.path.exists(NATIVE_PATH):
+        return False
+    LIB_PATH = NATIVE_PATH
+    return True
 
 
 def lib() -> ctypes.CDLL:

@@ -29,8 +29,18 @@ def compare(got_bf16, want_bf16):
     }
 
 
+# Every layer-output comparison of the session (name, absolute max-abs,
+# normalised max-abs, rel-L2); tests/conftest.py writes them to
+# gpurun_out/parity_metrics.json after a GPU session.
+RECORD = []
+
+
 def assert_close(got_bf16, want_bf16, what=""):
     m = compare(got_bf16, want_bf16)
+    RECORD.append({"what": what, "max_abs": m["max_abs"], "max_abs_norm": m["max_abs_norm"],
+                   "rel_l2": m["rel_l2"], "frac_exact": m["frac_exact"]})
     assert m["finite"], f"{what}: non-finite output"
-    assert m["max_abs_norm"] <= MAX_ABS and m["rel_l2"] <= REL_L2, f"{what}: {m}"
+    assert m["max_abs_norm"] <= MAX_ABS and m["rel_l2"] <= REL_L2, (
+        f"{what}: max_abs {m['max_abs']:.4g} (normalised {m['max_abs_norm']:.4g} <= {MAX_ABS}), "
+        f"rel_l2 {m['rel_l2']:.4g} (<= {REL_L2}); {m}")
     return m

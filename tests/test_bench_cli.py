@@ -12,3 +12,41 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=300, cwd=ROOT)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_rocminfo_peak_parser():
+    """bench.py derives the bf16 peak from rocminfo (CUs x max clock x 4096)."""
+    import bench
+    text = """*******
+Agent 1
+*******
+  Name:                    AMD EPYC 9575F
+  Compute Unit:            128
+  Max Clock Freq. (MHz):   3300
+*******
+Agent 2
+*******
+  Name:                    gfx950
+  Uuid:                    GPU-1234
+  Marketing Name:          AMD Instinct MI355X
+  Compute Unit:            256
+  Max Clock Freq. (MHz):   2400
+"""
+    assert bench.parse_rocminfo(text) == (256, 2400)
+    assert bench.parse_rocminfo("no agents") is None
+    cu, mhz = bench.parse_rocminfo(text)
+    assert abs(cu * mhz * 1e6 * 4096 / 1e12 - 2516.6) < 0.1
+
+
+def test_cpu_baseline_reports_native_build_and_host(tmp_path):
+    """The CPU baseline leg builds the oracle with the reference's runomp
+    flags for this host and names the CPU it ran on."""
+    import subprocess as sp
+    code = ("import sys; sys.path.insert(0, 'gpt-oss_amd'); import bench, synth, json; "
+            "print(json.dumps(bench.cpu_baseline(synth.make_data('c0_tiny'), 0.2)))")
+    r = sp.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300, cwd=ROOT)
+    assert r.returncode == 0, r.stderr
+    import json
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["kind"] == "port" and res["value"] > 0 and res["cores"] >= 1
+    assert "march=native" in res["build"] and res["cpu"] != ""
