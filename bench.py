@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="skip the C4 MoE-share line (24 layers at T = 512)")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -219,6 +221,60 @@ def time_layer(layers, x, args):
             "note": "both include a device copy of x per step (the layer updates x in place)"}
 
 
+def time_c4_moe_share(args, dev):
+    """The MoE share of config C4 (the 20B decoder step, 512 sequences): 24
+    gptoss_moe_layer calls (RMSNorm + MoE + residual, in place) at T = 512,
+    each layer with its own random MXFP4 weights (generated on the device,
+    packed, then only the packed copy kept: 24 x 425 MB).  An extra line, not
+    `value`."""
+    import torch
+    import gptoss_moe
+    L, H, D, E, K, T = 24, 2880, 2880, 32, 4, 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x6F55C4)
+    n1, n2 = E * 2 * D * H, E * H * D
+
+    def bf16(shape, sigma):
+        return (torch.randn(shape, generator=g, device=dev) * sigma).to(torch.bfloat16).view(torch.int16)
+
+    def u8(n, lo, hi):
+        return torch.randint(lo, hi, (n,), generator=g, device=dev, dtype=torch.uint8)
+    shape = gptoss_moe.make_shape(H, D, E, K)
+    layers, rms = [], []
+    for _ in range(L):
+        w = {"router_w": bf16((E, H), 0.02), "router_b": bf16((E,), 0.01),
+             "w1": u8(n1 // 2, 0, 256), "w1_scales": u8(n1 // 32, 120, 129), "b1": bf16((E, 2 * D), 0.01),
+             "w2": u8(n2 // 2, 0, 256), "w2_scales": u8(n2 // 32, 120, 129), "b2": bf16((E, H), 0.01)}
+        lay = gptoss_moe.MoeLayer(shape, w, T, dev)
+        lay.drop_unpacked()
+        layers.append(lay)
+        rms.append(bf16((H,), 0.1).view(torch.bfloat16).float().add(1).to(torch.bfloat16).view(torch.int16))
+    x0 = bf16((T, H), 1.0)
+    x = x0.clone()
+    t = torch.empty_like(x)
+
+    def step():
+        for l in range(L):
+            layers[l].layer(x, rms[l], t_scratch=t)
+    for _ in range(max(1, args.warmup)):
+        x.copy_(x0)
+        step()
+    torch.cuda.synchronize()
+    steps = max(3, args.steps // 5)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        x.copy_(x0)
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": "c4 MoE share: 24 x gptoss_moe_layer, 20B shape, T = 512, per-layer weights",
+            "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / L, 1),
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "steps": steps,
+            "note": "includes one device copy of x per step (the layers update x in place)"}
+
+
 def time_variants(layers, x, out, fi, fw, args, c, flops):
     """Extra measured variants (never the headline): the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
@@ -375,6 +431,13 @@ def main():
         res["layer_entry"] = time_layer(layers, x, args)
     if not args.no_variants:
         res["variants"] = time_variants(layers, x, out, fi, fw, args, c, flops)
+    if not args.no_c4 and c.name == "c1_20b_decode":
+        del layers, base
+        torch.cuda.empty_cache()
+        try:
+            res["c4_moe_share"] = time_c4_moe_share(args, dev)
+        except Exception as e:  # an extra line: report, never fail the headline
+            res["c4_moe_share"] = {"error": f"{type(e).__name__}: {e}"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
     else:
