@@ -42,6 +42,11 @@ _SIGS = {
     "orc_e4m3_dec": (_F, [ctypes.c_uint8]),
     "orc_moe_fp32_token": (None, [_I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "orc_num_threads": (_I, []),
+    "orc_f2h": (ctypes.c_uint16, [_F]),
+    "orc_h2f": (_F, [ctypes.c_uint16]),
+    "orc_kv_quantize_row": (None, [_P, _I, _P, _P]),
+    "orc_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
 }
 
 _lib = None
@@ -254,3 +259,46 @@ class Fp32Engine:
 
 def num_threads() -> int:
     return lib().orc_num_threads()
+
+
+# ------------------------------------------------------------ attention --
+
+def f2h(x: float) -> int:
+    return int(lib().orc_f2h(float(x)))
+
+
+def kv_quantize_rows(x):
+    """bf16 rows [n][kv_dim] -> (int8 codes [n][kv_dim], fp16 scale bits [n])
+    (attention.hpp:582-628)."""
+    x = _c(x, np.uint16)
+    n, kv = x.shape
+    q = np.empty((n, kv), np.int8)
+    s = np.empty(n, np.uint16)
+    L = lib()
+    for i in range(n):
+        L.orc_kv_quantize_row(_p(x[i]), kv, _p(q[i]), _p(s[i:i + 1]))
+    return q, s
+
+
+def attn_decode(q, kq, vq, ks, vs, kb, vb, sinks, pos, *, n_kv_heads: int, layer_idx: int,
+                sliding_window: int, keep: int, prefix_rule: int = 0,
+                phi_splits: int = 0) -> np.ndarray:
+    """Decode attention over logical caches (attn_oracle.c): q bf16
+    [B][n_heads][hd]; kq/vq int8 [B][cap][kv_dim]; ks/vs fp16 bits [B][cap];
+    kb/vb bf16 [B][keep][kv_dim] or None; sinks bf16 [n_heads]; pos int32 [B].
+    Returns fp32 [B][n_heads][hd]."""
+    q = _c(q, np.uint16)
+    B, NH, HD = q.shape
+    kq, vq = _c(kq, np.int8), _c(vq, np.int8)
+    cap = kq.shape[1]
+    ks, vs = _c(ks, np.uint16), _c(vs, np.uint16)
+    kb = None if kb is None else _c(kb, np.uint16)
+    vb = None if vb is None else _c(vb, np.uint16)
+    sinks, pos = _c(sinks, np.uint16), _c(pos, np.int32)
+    out = np.empty((B, NH, HD), np.float32)
+    rc = lib().orc_attn_decode(B, NH, n_kv_heads, HD, cap, layer_idx, sliding_window, keep,
+                               prefix_rule, phi_splits, _p(q), _p(kq), _p(vq), _p(ks), _p(vs),
+                               _p(kb), _p(vb), _p(sinks), _p(pos), _p(out))
+    if rc != 0:
+        raise ValueError("orc_attn_decode: shape outside the restatement")
+    return out
