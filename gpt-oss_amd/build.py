@@ -1,4 +1,5 @@
-"""Build libgptoss_moe.so in-tree for gfx950 (hipcc, no JIT cache)."""
+"""Build libgptoss_moe.so and libgptoss_attn.so in-tree for gfx950 (hipcc, no
+JIT cache)."""
 from __future__ import annotations
 
 import os
@@ -18,6 +19,8 @@ HIP_FLAGS = [
 
 SOURCES = [os.path.join(HERE, "csrc", "gptoss_moe.hip"), os.path.join(HERE, "csrc", "bin_loader.cpp")]
 LIB = os.path.join(HERE, "libgptoss_moe.so")
+ATTN_SOURCES = [os.path.join(HERE, "csrc", "gptoss_attn.hip")]
+ATTN_LIB = os.path.join(HERE, "libgptoss_attn.so")
 
 
 # A C++ caller of the library and of the moe_gpu shim (csrc/moe_gpu_shim.hpp),
@@ -38,6 +41,7 @@ def _run(cmd, verbose):
 
 def build(verbose: bool = False) -> str:
     _run([HIPCC, *HIP_FLAGS, *SOURCES, "-o", LIB], verbose)
+    _run([HIPCC, *HIP_FLAGS, *ATTN_SOURCES, "-o", ATTN_LIB], verbose)
     os.makedirs(os.path.dirname(SHIM_TEST_BIN), exist_ok=True)
     _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -1,0 +1,176 @@
+"""Host-side mirror of the reference's decode-attention cache and kernels over
+the C ABI in include/gptoss_attn.h (libgptoss_attn.so, built from
+csrc/gptoss_attn.hip).
+
+`KvCache` owns GPURunState's attention caches (getp-csrc/getp_run.cpp:104-112,
+:443-486) for `n_seqs` sequences and every layer, with the reference's
+strides: per sequence, even layers hold `sliding_window` rows and odd layers
+`max_ctx` rows of kv_dim int8 codes, one fp16 scale per row, and odd layers'
+first `keep` tokens again in bf16.  `kv_update` and `decode` are the two
+kernel launches of attention_gpu (getp_run.cpp:2326-2470).  torch tensors
+serve as device memory only; there is no fallback: a missing library or a
+failed call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgptoss_attn.so")
+
+OK = 0
+ERR_INVALID_ARG = -1
+ERR_WORKSPACE = -2
+ERR_HIP = -3
+PREFIX_REFERENCE = 0
+PREFIX_MIXED = 1
+N_HEADS, N_KV_HEADS, HEAD_DIM = 64, 8, 64
+KV_DIM = N_KV_HEADS * HEAD_DIM
+
+
+class AttnError(RuntimeError):
+    def __init__(self, fn: str, rc: int, hip: int = 0):
+        super().__init__(f"{fn} failed: {rc}" + (f", hipError {hip}" if rc == ERR_HIP else ""))
+        self.rc = rc
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_heads", "n_kv_heads", "head_dim", "n_layers",
+                                            "sliding_window", "keep", "prefix_rule")]
+
+
+class Cache(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("key_codes", "value_codes", "key_scales",
+                                               "value_scales", "key_bf16", "value_bf16")] + [
+        ("batch_kv_stride", ctypes.c_size_t), ("batch_scale_stride", ctypes.c_size_t)]
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [("layer_idx", ctypes.c_int), ("cap", ctypes.c_int),
+                ("layer_kv_offset", ctypes.c_size_t), ("layer_scale_offset", ctypes.c_size_t)]
+
+
+_P = ctypes.c_void_p
+_SIGS = {
+    "gptoss_attn_kv_update": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_int, _P]),
+    "gptoss_attn_workspace_size": (ctypes.c_size_t, [_P, ctypes.c_int, ctypes.c_int]),
+    "gptoss_attn_decode": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P,
+                                          ctypes.c_size_t, _P]),
+    "gptoss_attn_last_hip_error": (ctypes.c_int, []),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(fn: str, rc: int) -> None:
+    if rc != OK:
+        raise AttnError(fn, rc, load_library().gptoss_attn_last_hip_error())
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def layer_caps(n_layers: int, sliding_window: int, max_ctx: int):
+    """Rows per layer (getp_run.cpp:293-296): even layers a ring of
+    sliding_window rows when there is a window, else max_ctx."""
+    return [sliding_window if (l % 2 == 0 and sliding_window > 0) else max_ctx
+            for l in range(n_layers)]
+
+
+class KvCache:
+    def __init__(self, n_seqs: int, n_layers: int, max_ctx: int, sliding_window: int = 128,
+                 keep: int = 16, prefix_rule: int = PREFIX_REFERENCE, device="cuda"):
+        import torch
+        if max_ctx % 16 or sliding_window % 16 or keep % 16:
+            raise ValueError("max_ctx, sliding_window and keep must be multiples of 16")
+        self.lib = load_library()
+        self.n_seqs, self.n_layers, self.max_ctx = n_seqs, n_layers, max_ctx
+        self.shape = Shape(N_HEADS, N_KV_HEADS, HEAD_DIM, n_layers, sliding_window, keep,
+                           prefix_rule)
+        self.caps = layer_caps(n_layers, sliding_window, max_ctx)
+        self.offsets = [sum(self.caps[:l]) for l in range(n_layers)]
+        rows = sum(self.caps)
+        self.rows = rows
+        self.key_codes = torch.zeros(n_seqs * rows * KV_DIM, dtype=torch.int8, device=device)
+        self.value_codes = torch.zeros_like(self.key_codes)
+        self.key_scales = torch.zeros(n_seqs * rows, dtype=torch.int16, device=device)
+        self.value_scales = torch.zeros_like(self.key_scales)
+        nb = max(1, n_seqs * n_layers * keep * KV_DIM)
+        self.key_bf16 = torch.zeros(nb, dtype=torch.int16, device=device)
+        self.value_bf16 = torch.zeros_like(self.key_bf16)
+        self.cache = Cache(self.key_codes.data_ptr(), self.value_codes.data_ptr(),
+                           self.key_scales.data_ptr(), self.value_scales.data_ptr(),
+                           self.key_bf16.data_ptr() if keep else None,
+                           self.value_bf16.data_ptr() if keep else None,
+                           rows * KV_DIM, rows)
+        ws = self.lib.gptoss_attn_workspace_size(ctypes.byref(self.shape), max(self.caps), n_seqs)
+        self.ws = torch.empty(max(ws // 4, 1), dtype=torch.float32, device=device) if ws else None
+        self.ws_bytes = ws
+
+    def layer(self, l: int) -> Layer:
+        return Layer(l, self.caps[l], self.offsets[l] * KV_DIM, self.offsets[l])
+
+    def kv_update(self, l: int, k, v, pos, n_seqs=None, stream=None) -> None:
+        """k, v: bf16 [n][512] (torch bfloat16/int16, device); pos int32 [n]."""
+        n = self.n_seqs if n_seqs is None else n_seqs
+        L = self.layer(l)
+        _check("gptoss_attn_kv_update",
+               self.lib.gptoss_attn_kv_update(ctypes.byref(self.shape), ctypes.byref(self.cache),
+                                              ctypes.byref(L), k.data_ptr(), v.data_ptr(),
+                                              pos.data_ptr(), n, _stream(stream)))
+
+    def decode(self, l: int, q, sinks, pos, out=None, n_seqs=None, split=True, stream=None):
+        """q: bf16 [n][64][64]; sinks bf16 [64]; returns out bf16 [n][64][64]."""
+        import torch
+        n = self.n_seqs if n_seqs is None else n_seqs
+        if out is None:
+            out = torch.empty((n, N_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+        L = self.layer(l)
+        ws = self.ws if split else None
+        _check("gptoss_attn_decode",
+               self.lib.gptoss_attn_decode(ctypes.byref(self.shape), ctypes.byref(self.cache),
+                                           ctypes.byref(L), q.data_ptr(), sinks.data_ptr(),
+                                           pos.data_ptr(), n, out.data_ptr(),
+                                           None if ws is None else ws.data_ptr(),
+                                           self.ws_bytes if ws is not None else 0,
+                                           _stream(stream)))
+        return out
+
+    def layer_slabs(self, l: int):
+        """This layer's raw slabs per sequence, as CPU numpy arrays: key codes,
+        value codes [n][cap * 512] (library tile order), scales [n][cap], and
+        bf16 rows [n][keep * 512] (odd layers)."""
+        import numpy as np
+        rows, cap, off = self.rows, self.caps[l], self.offsets[l]
+        kc = self.key_codes.view(self.n_seqs, rows * KV_DIM)[:, off * KV_DIM:(off + cap) * KV_DIM]
+        vc = self.value_codes.view(self.n_seqs, rows * KV_DIM)[:, off * KV_DIM:(off + cap) * KV_DIM]
+        ks = self.key_scales.view(self.n_seqs, rows)[:, off:off + cap]
+        vs = self.value_scales.view(self.n_seqs, rows)[:, off:off + cap]
+        keep = self.shape.keep
+        kb = self.key_bf16[:self.n_seqs * self.n_layers * keep * KV_DIM].view(
+            self.n_seqs, self.n_layers, keep * KV_DIM)[:, l] if keep else None
+        vb = self.value_bf16[:self.n_seqs * self.n_layers * keep * KV_DIM].view(
+            self.n_seqs, self.n_layers, keep * KV_DIM)[:, l] if keep else None
+        cpu = lambda t: None if t is None else t.cpu().numpy()
+        return (cpu(kc), cpu(vc), cpu(ks).view(np.uint16), cpu(vs).view(np.uint16),
+                None if kb is None else cpu(kb).view(np.uint16),
+                None if vb is None else cpu(vb).view(np.uint16))

@@ -1,0 +1,107 @@
+"""The decode-attention library loads, exports every function
+include/gptoss_attn.h declares and rejects bad arguments with status codes
+before any launch, without a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import gptoss_attn as ga
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gptoss_attn.h")
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    return sorted(set(re.findall(r"\b(gptoss_attn_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ga.load_library()
+    names = declared_functions()
+    assert len(names) == 4
+    assert not [n for n in names if not hasattr(lib, n)]
+    assert set(names) <= set(ga._SIGS)
+
+
+def shape(**kw):
+    d = dict(n_heads=64, n_kv_heads=8, head_dim=64, n_layers=24, sliding_window=128, keep=16,
+             prefix_rule=0)
+    d.update(kw)
+    return ga.Shape(*[d[n] for n, _ in ga.Shape._fields_])
+
+
+def test_workspace_size():
+    lib = ga.load_library()
+    s = shape()
+    # 512 sequences x 8 KV heads fill the chip: no split, no workspace
+    assert lib.gptoss_attn_workspace_size(ctypes.byref(s), 1024, 512) == 0
+    # one sequence: splits of >= 4 blocks of 16 rows, at most 64
+    one = lib.gptoss_attn_workspace_size(ctypes.byref(s), 1024, 1)
+    assert one == 1 * 8 * 16 * (16 + 512) * 4
+    assert lib.gptoss_attn_workspace_size(ctypes.byref(s), 128, 1) == 8 * 2 * 528 * 4
+    assert lib.gptoss_attn_workspace_size(ctypes.byref(shape(head_dim=128)), 1024, 1) == 0
+
+
+class FakeCache:
+    """Non-null, aligned fake device addresses: the calls must reject before
+    touching them."""
+
+    def __init__(self, rows=128 + 1024, **kw):
+        base = 1 << 30
+        self.c = ga.Cache(base, base + (1 << 24), base + (2 << 24), base + (3 << 24),
+                          base + (4 << 24), base + (5 << 24), rows * 512, rows)
+        for k, v in kw.items():
+            setattr(self.c, k, v)
+
+
+def call_both(s, cache, layer, n=4):
+    lib = ga.load_library()
+    p = 1 << 20
+    a = lib.gptoss_attn_kv_update(ctypes.byref(s), ctypes.byref(cache), ctypes.byref(layer), p, p,
+                                  p, n, None)
+    b = lib.gptoss_attn_decode(ctypes.byref(s), ctypes.byref(cache), ctypes.byref(layer), p, p, p,
+                               n, p, None, 0, None)
+    return a, b
+
+
+@pytest.mark.parametrize("bad", [dict(n_heads=32), dict(n_kv_heads=4), dict(head_dim=128),
+                                 dict(sliding_window=100), dict(keep=10), dict(prefix_rule=2),
+                                 dict(n_layers=0)])
+def test_bad_shapes_rejected(bad):
+    c = FakeCache().c
+    assert call_both(shape(**bad), c, ga.Layer(0, 128, 0, 0)) == (ga.ERR_INVALID_ARG,) * 2
+
+
+@pytest.mark.parametrize("layer,cache_kw", [
+    (ga.Layer(0, 64, 0, 0), {}),                       # ring layer smaller than the window
+    (ga.Layer(1, 1000, 128 * 512, 128), {}),           # cap not a multiple of 16
+    (ga.Layer(1, 1024, 100, 128), {}),                 # misaligned layer offset
+    (ga.Layer(1, 1024, 128 * 512, 128), dict(batch_kv_stride=1024 * 512)),   # slab past the stride
+    (ga.Layer(1, 1024, 128 * 512, 128), dict(batch_scale_stride=1024)),
+    (ga.Layer(1, 1024, 128 * 512, 128), dict(key_bf16=None)),                # odd layer, keep > 0
+    (ga.Layer(1, 1024, 128 * 512, 128), dict(key_codes=(1 << 30) + 8)),      # misaligned codes
+    (ga.Layer(24, 128, 0, 0), {}),                     # layer index out of range
+    (ga.Layer(1, 8, 128 * 512, 128), {}),              # keep > cap
+])
+def test_bad_layers_rejected(layer, cache_kw):
+    c = FakeCache(**cache_kw).c
+    assert call_both(shape(), c, layer) == (ga.ERR_INVALID_ARG,) * 2
+
+
+def test_bad_buffers_rejected():
+    lib = ga.load_library()
+    s, c, L = shape(), FakeCache().c, ga.Layer(0, 128, 0, 0)
+    p = 1 << 20
+    assert lib.gptoss_attn_kv_update(ctypes.byref(s), ctypes.byref(c), ctypes.byref(L), None, p, p,
+                                     4, None) == ga.ERR_INVALID_ARG
+    assert lib.gptoss_attn_decode(ctypes.byref(s), ctypes.byref(c), ctypes.byref(L), p + 2, p, p,
+                                  4, p, None, 0, None) == ga.ERR_INVALID_ARG
+    assert lib.gptoss_attn_decode(ctypes.byref(s), ctypes.byref(c), ctypes.byref(L), p, p, p, 4, p,
+                                  p + 64, 4096, None) == ga.ERR_WORKSPACE
+    assert lib.gptoss_attn_decode(ctypes.byref(s), ctypes.byref(c), ctypes.byref(L), p, p, p, -1,
+                                  p, None, 0, None) == ga.ERR_INVALID_ARG
+    # zero sequences: nothing to do
+    assert call_both(s, c, L, n=0) == (ga.OK, ga.OK)

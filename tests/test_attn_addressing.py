@@ -1,0 +1,215 @@
+"""CPU mirror of the decode-attention kernels (gptoss_attn.hip) at the lane
+level: the cache update's stores, the decode kernel's loads, its
+matrix-instruction operand layout (v_mfma_f32_16x16x32_bf16: lane l supplies
+A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16], and receives
+D[4 (l / 16) + i][l % 16]) and its online softmax, checked against the
+oracle.  A wrong tile order, lane mapping, mask or split bound fails here
+without a GPU, and every offset is checked against its buffer."""
+import numpy as np
+import pytest
+
+import oracle
+from attn_cases import N_HEADS, make_case, oracle_out
+from attn_layout import HD, KV, N_KV, TILE, from_logical, key_offset, to_logical, value_offset
+from synth import bf16_to_f32, f32_to_bf16
+
+LANE = np.arange(64)
+C, G = LANE % 16, LANE // 16
+LOG2E = np.float32(1.4426950408889634)
+
+
+def test_layout_maps_are_bijections():
+    rows = 48
+    r, gd = np.meshgrid(np.arange(rows), np.arange(KV), indexing="ij")
+    for f in (key_offset, value_offset):
+        o = f(r, gd // HD, gd % HD).ravel()
+        assert np.array_equal(np.sort(o), np.arange(rows * KV))
+
+
+def test_kv_update_lane_stores_match_layout():
+    """kv_update_kernel: lane l stores key bytes (r % 16) * 64 + d0 .. +7 and
+    value bytes v_tile_off(r, d0 + j) of tile ((r / 16) * 8 + l / 8)."""
+    for r in (0, 5, 16, 127, 1000):
+        tile = ((r >> 4) * N_KV + (LANE >> 3)) * TILE
+        d0 = 8 * (LANE & 7)
+        for j in range(8):
+            d = d0 + j
+            g = LANE >> 3
+            assert np.array_equal(tile + (r & 15) * 64 + d, key_offset(r, g, d))
+            vt = (d & 15) * 64 + ((r & 15) >> 2) * 16 + (d >> 4) * 4 + (r & 3)
+            assert np.array_equal(tile + vt, value_offset(r, g, d))
+
+
+def mfma(a_lanes, b_lanes, acc):
+    """v_mfma_f32_16x16x32_bf16 on per-lane operands [64][8] (fp32 values)."""
+    A = np.zeros((16, 32), np.float64)
+    B = np.zeros((32, 16), np.float64)
+    for l in range(64):
+        A[l % 16, 8 * (l // 16):8 * (l // 16) + 8] = a_lanes[l]
+        B[8 * (l // 16):8 * (l // 16) + 8, l % 16] = b_lanes[l]
+    D = A @ B
+    out = acc.astype(np.float64).copy()
+    for l in range(64):
+        out[l] += D[4 * (l // 16):4 * (l // 16) + 4, l % 16]
+    return out.astype(np.float32)
+
+
+def bf16r(x):
+    return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32)))
+
+
+def decode_mirror(c, S, rule, slabs):
+    """attn_decode_kernel + attn_combine_kernel for case c with S splits;
+    slabs: per sequence, the library-layout key, value, bf16 key and bf16
+    value slabs of the layer."""
+    B = c.B
+    out = np.zeros((B, N_HEADS, HD), np.float32)
+    for b in range(B):
+        slab_k, slab_v, kb_slab, vb_slab = (x[b] for x in slabs)
+        pos = int(c.pos[b])
+        ring = c.even() and c.window > 0
+        nvalid = min(pos + 1, c.window) if ring else pos + 1
+        nblk = (nvalid + 15) >> 4
+        nb16 = 0
+        if not c.even() and c.keep > 0:
+            nb16 = (nblk if pos < c.keep else 0) if rule == 0 else min(nblk, c.keep >> 4)
+        ksf = c.ks[b].view(np.float16).astype(np.float32)
+        vsf = c.vs[b].view(np.float16).astype(np.float32)
+        for kvh in range(N_KV):
+            parts = []
+            for s in range(S):
+                blk0, blk1 = nblk * s // S, nblk * (s + 1) // S
+                qv = np.zeros((64, 16), np.float32)
+                heads = kvh * 8 + C
+                m = C < 8
+                qf = bf16_to_f32(c.q[b]).astype(np.float32)
+                for l in range(64):
+                    if m[l]:
+                        qv[l] = qf[heads[l], 16 * G[l]:16 * G[l] + 16]
+                q0, q1 = qv[:, :8], qv[:, 8:]
+                M = np.full(64, -np.inf, np.float32)
+                Ls = np.zeros(64, np.float32)
+                O = np.zeros((4, 64, 4), np.float32)
+
+                def block_ops(blk, bf16):
+                    if blk is None:
+                        return None
+                    t = (blk * N_KV + kvh) * TILE
+                    if bf16:
+                        ko = t + C * 64 + 16 * G
+                        assert ko.max() + 16 <= kb_slab.size
+                        kk = np.stack([bf16_to_f32(kb_slab[o:o + 16]) for o in ko])
+                        vv = np.stack([bf16_to_f32(vb_slab[o:o + 16]) for o in ko])
+                        ksc = np.full((64, 4), np.float32(0.125) * LOG2E, np.float32)
+                        vsc = np.ones((64, 4), np.float32)
+                    else:
+                        ko = t + C * 64 + 16 * G
+                        assert ko.max() + 16 <= slab_k.size
+                        kk = np.stack([slab_k[o:o + 16] for o in ko]).astype(np.float32)
+                        vv = np.stack([slab_v[o:o + 16] for o in ko]).astype(np.float32)
+                        so = blk * 16 + 4 * G
+                        assert so.max() + 4 <= c.cap
+                        ksc = np.stack([ksf[o:o + 4] for o in so]) * (np.float32(0.125) * LOG2E)
+                        vsc = np.stack([vsf[o:o + 4] for o in so])
+                    # value operand per dim tile: elements dt * 4 + i
+                    vop = [vv[:, 4 * dt:4 * dt + 4] for dt in range(4)]
+                    return kk[:, :8], kk[:, 8:], vop, ksc.astype(np.float32), vsc.astype(np.float32)
+
+                def step(blk, nb, bf16):
+                    nonlocal M, Ls, O
+                    A = block_ops(blk, bf16)
+                    Bo = block_ops(blk + 1, bf16) if nb > 1 else None
+                    s0 = mfma(A[1], q1, mfma(A[0], q0, np.zeros((64, 4), np.float32)))
+                    s1 = mfma(Bo[1], q1, mfma(Bo[0], q0, np.zeros((64, 4), np.float32))) if Bo else np.zeros((64, 4), np.float32)
+                    row0 = blk * 16 + 4 * G
+                    ok = np.zeros((64, 8), bool)
+                    sv = np.full((64, 8), -np.inf, np.float32)
+                    for i in range(4):
+                        ok[:, i] = row0 + i < nvalid
+                        ok[:, 4 + i] = (nb > 1) & (row0 + 16 + i < nvalid)
+                        sv[:, i] = np.where(ok[:, i], s0[:, i] * A[3][:, i], -np.inf)
+                        if Bo:
+                            sv[:, 4 + i] = np.where(ok[:, 4 + i], s1[:, i] * Bo[3][:, i], -np.inf)
+                    bm = sv.max(1)
+                    bm = np.maximum(bm, bm[LANE ^ 16])
+                    bm = np.maximum(bm, bm[LANE ^ 32])
+                    mn = np.maximum(M, bm)
+                    alpha = np.exp2(M - mn)
+                    p = np.exp2(sv - mn[:, None])
+                    Ls = Ls * alpha + p.sum(1)
+                    M = mn
+                    vsc = np.concatenate([A[4], Bo[4] if Bo else np.zeros((64, 4), np.float32)], 1)
+                    pop = bf16r(np.where(ok, p * vsc, 0))
+                    ar = np.stack([alpha[4 * G + i] for i in range(4)], 1)
+                    for dt in range(4):
+                        va = A[2][dt]
+                        vb = Bo[2][dt] if Bo else np.zeros((64, 4), np.float32)
+                        vop = np.concatenate([va, vb], 1)
+                        if bf16:
+                            vop = np.where(ok, vop, 0)
+                        O[dt] = mfma(pop, vop, O[dt] * ar)
+
+                e16 = min(blk1, nb16)
+                for blk in range(blk0, e16, 2):
+                    step(blk, min(2, e16 - blk), True)
+                for blk in range(max(blk0, nb16), blk1, 2):
+                    step(blk, min(2, blk1 - blk), False)
+                L = Ls + Ls[LANE ^ 16]
+                L = L + L[LANE ^ 32]
+                # partial: m, l of heads 0..7, O rows 4g + i for g < 2
+                o_rows = np.zeros((8, HD), np.float32)
+                for l in range(32):
+                    for dt in range(4):
+                        for i in range(4):
+                            o_rows[4 * G[l] + i, 16 * dt + C[l]] = O[dt][l, i]
+                parts.append((M[:8].copy(), L[:8].copy(), o_rows))
+            mm = np.max([p[0] for p in parts], 0)
+            Lt = np.zeros(8, np.float32)
+            ot = np.zeros((8, HD), np.float32)
+            for pm, pl, po in parts:
+                w = np.exp2(pm - mm)
+                Lt += pl * w
+                ot += po * w[:, None]
+            sk = bf16_to_f32(c.sinks[kvh * 8:kvh * 8 + 8]) * LOG2E
+            mf = np.maximum(mm, sk)
+            al = np.exp2(mm - mf)
+            f = al / (Lt * al + np.exp2(sk - mf))
+            out[b, kvh * 8:kvh * 8 + 8] = ot * f[:, None]
+    return out
+
+
+def library_slabs(c):
+    """The caches in the library's layout (one layer slab per sequence)."""
+    sk, sv, kbs, vbs = [], [], [], []
+    for b in range(c.B):
+        k, v = from_logical(c.kq[b], c.vq[b])
+        sk.append(k)
+        sv.append(v)
+        kb, vb = from_logical(c.kb[b], c.vb[b]) if c.keep else (np.zeros(0, np.uint16),) * 2
+        kbs.append(kb)
+        vbs.append(vb)
+    return sk, sv, kbs, vbs
+
+
+@pytest.mark.parametrize("layer,pos,keep,S,rule", [
+    (0, [0, 17, 200], 16, 1, 0),
+    (0, [127, 5], 16, 3, 0),
+    (1, [9, 40], 16, 1, 0),
+    (1, [9, 40, 70], 16, 2, 1),
+    (3, [130], 128, 4, 1),
+])
+def test_decode_mirror_matches_oracle(layer, pos, keep, S, rule):
+    c = make_case(31 + layer, layer_idx=layer, pos=pos, keep=keep,
+                  cap=None if layer % 2 == 0 else 16 * ((max(pos) + 16) // 16))
+    slabs = library_slabs(c)
+    # round trip of the layout helpers
+    for b in range(c.B):
+        lk, lv = to_logical(slabs[0][b], slabs[1][b], c.cap)
+        assert np.array_equal(lk, c.kq[b]) and np.array_equal(lv, c.vq[b])
+    got = decode_mirror(c, S, rule, slabs)
+    want = oracle_out(c, prefix_rule=rule)
+    err = np.abs(got - want)
+    assert err.max() <= 2e-2 * max(1.0, np.abs(want).max()), err.max()
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 4e-3, rel
+
