@@ -39,7 +39,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c4", action="store_true",
-                    help="skip the C4 MoE-share line (24 layers at T = 512)")
+                    help="skip the C4 MoE-share and attention lines (24 layers at 512 tokens)")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="only the C4 attention line (decode attention over the int8 KV cache)")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -275,6 +277,76 @@ def time_c4_moe_share(args, dev):
             "note": "includes one device copy of x per step (the layers update x in place)"}
 
 
+def attn_layer_bytes(n_seqs: int, rows: int, bf16_rows: int) -> int:
+    """Algorithmic HBM bytes of one decode-attention call: per sequence, the
+    int8 key and value rows with their fp16 scales (1028 B per row), the bf16
+    rows (2048 B per row), the query and the output (8 KiB each)."""
+    return n_seqs * ((rows - bf16_rows) * 1028 + bf16_rows * 2048 + 2 * 8192)
+
+
+def time_c4_attention(args, dev):
+    """The attention share of config C4: per decode step, 24 layers of
+    (KV-cache update + decode attention) for 512 sequences at context 1024;
+    even layers a 128-row sliding-window ring, odd layers the full context
+    with the first 128 tokens kept in bf16.  Caches are filled once with
+    random rows; each timed step rewrites the current token's row and
+    attends.  An extra line, not `value`."""
+    import torch
+    import gptoss_attn as ga
+    B, L, ctx, W, keep = 512, 24, 1024, 128, 128
+    kc = ga.KvCache(B, L, ctx, sliding_window=W, keep=keep, prefix_rule=ga.PREFIX_MIXED, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0xA77E)
+    pool = [(torch.randn((B, ga.KV_DIM), generator=g, device=dev).to(torch.bfloat16),
+             torch.randn((B, ga.KV_DIM), generator=g, device=dev).to(torch.bfloat16)) for _ in range(4)]
+    for t in range(ctx):
+        pos = torch.full((B,), t, dtype=torch.int32, device=dev)
+        k, v = pool[t % 4]
+        for l in range(L):
+            kc.kv_update(l, k, v, pos)
+    pos = torch.full((B,), ctx - 1, dtype=torch.int32, device=dev)
+    q = torch.randn((B, 64, 64), generator=g, device=dev).to(torch.bfloat16)
+    sinks = torch.randn((L, 64), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty((B, 64, 64), dtype=torch.bfloat16, device=dev)
+    k, v = pool[0]
+
+    def step(update=True):
+        for l in range(L):
+            if update:
+                kc.kv_update(l, k, v, pos)
+            kc.decode(l, q, sinks[l], pos, out=out)
+
+    def timed(fn, n):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+    steps = max(3, args.steps // 5)
+    ms_step = timed(step, steps)
+    ms_decode = timed(lambda: step(False), steps)
+    ms_odd = timed(lambda: kc.decode(1, q, sinks[1], pos, out=out), 20)
+    ms_even = timed(lambda: kc.decode(0, q, sinks[0], pos, out=out), 20)
+    b_odd = attn_layer_bytes(B, ctx, keep)
+    b_even = attn_layer_bytes(B, W, 0)
+    b_step = (L // 2) * (b_odd + b_even)
+    gbs = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 1)
+    return {"workload": "c4 attention share: 24 x (KV update + decode attention), 512 sequences, "
+                        "context 1024, window 128 on even layers, 128 bf16 tokens on odd layers",
+            "ms_per_step": round(ms_step, 4), "decode_only_ms_per_step": round(ms_decode, 4),
+            "tokens_per_s": round(B / (ms_step * 1e-3), 1), "steps": steps,
+            "odd_layer_us": round(ms_odd * 1e3, 2), "even_layer_us": round(ms_even * 1e3, 2),
+            "algorithmic_bytes": {"odd_layer": b_odd, "even_layer": b_even, "step": b_step},
+            "hbm_gbs": {"odd_layer": gbs(b_odd, ms_odd), "even_layer": gbs(b_even, ms_even),
+                        "decode_step": gbs(b_step, ms_decode)},
+            "hbm_frac_odd_layer": round(b_odd / (ms_odd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def time_variants(layers, x, out, fi, fw, args, c, flops):
     """Extra measured variants (never the headline): the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
@@ -329,6 +401,9 @@ def main():
     import synth
 
     dev = torch.device("cuda:0")
+    if args.attn_only:
+        print(json.dumps({"c4_attention": time_c4_attention(args, dev)}))
+        return
     d = synth.make_data(args.config)
     c = d.cfg
     layer_bytes = d.weight_bytes
@@ -438,6 +513,10 @@ def main():
             res["c4_moe_share"] = time_c4_moe_share(args, dev)
         except Exception as e:  # an extra line: report, never fail the headline
             res["c4_moe_share"] = {"error": f"{type(e).__name__}: {e}"}
+        try:
+            res["c4_attention"] = time_c4_attention(args, dev)
+        except Exception as e:  # an extra line: report, never fail the headline
+            res["c4_attention"] = {"error": f"{type(e).__name__}: {e}"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
     else:
