@@ -12,19 +12,24 @@
 //                      attention_mfma.hpp:1113-1460);
 //   attn_combine_kernel merges the splits when there are several.
 //
-// Matrix-core mapping (v_mfma_f32_16x16x32_bf16, lane = c + 16 g):
-//   scores  S[token][head] = K[16 tokens][64 dims] . Q^T, two k-steps; lane
-//           (c, g) supplies key row c, dims 16g..16g+15 (one 16-byte load of
-//           the tile, int8 -> bf16 exactly) and query head c, the same dims;
-//           query heads 8..15 of the instruction are zero.  The result gives
-//           lane (c, g) head c at tokens 4g..4g+3.
-//   output  O[head][dim] += P'[head][32 tokens] . V[32 tokens][16 dims] for
-//           4 dim tiles; P' = p * value_scale (bf16) is exactly the score
-//           layout of two 16-token blocks, and the value tile order gives
-//           lane (c, g) dims 16 dt + c at tokens 4g..4g+3 of a block in one
-//           16-byte load.  Rows 4g..4g+3 of the result are heads (g < 2).
-// Keys and values are exact in bf16 (|code| <= 127); q . k is accumulated in
-// fp32 and scaled by the token's key scale / 8 afterwards.
+// Matrix-core mapping (lane = c + 16 g; every instruction is 16x16, lane
+// (c, g) receives rows 4g..4g+3 of column c of the result):
+//   scores  S[token][head] = K[16 tokens][64 dims] . Q^T on
+//           v_mfma_i32_16x16x64_i8: lane (c, g) supplies key row c, dims
+//           16g..16g+15 (the 16 raw bytes of the tile, no conversion) and
+//           query head c, the same dims, as Q = rint(q 2^E) = 256 hi + lo
+//           (two instructions, exact in int32; |Q| < 2^14, E per head, so Q
+//           carries q to 2^-14 of the head's largest element).  Heads 8..15
+//           of the instruction are zero.  Lane (c, g) gets head c at tokens
+//           4g..4g+3; the score is S * key scale * 2^-E * log2(e) / 8.
+//   output  O[head][dim] += P'[head][32 tokens] . V[32 tokens][16 dims] on
+//           v_mfma_f32_16x16x32_bf16 for 4 dim tiles: P' = p * value scale
+//           (bf16) is the score layout of two 16-token blocks, and the value
+//           tile order gives lane (c, g) dims 16 dt + c at tokens 4g..4g+3 of
+//           a block in one 16-byte load (int8 -> bf16 exactly).  Rows 4g..4g+3
+//           of the result are heads (g < 2).
+// bf16-kept blocks use v_mfma_f32_16x16x32_bf16 for the scores with the bf16
+// query itself.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
@@ -39,6 +44,9 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 
 constexpr int kKvHeads = 8;      // n_kv_heads
 constexpr int kGqa = 8;          // query heads per KV head
@@ -59,32 +67,63 @@ int hip_fail(hipError_t e) {
 
 __device__ inline float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ inline uint32_t f2bf(float f) {  // round to nearest even; finite inputs
-    const uint32_t u = __float_as_uint(f);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
 __device__ inline float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 __device__ inline uint16_t f2h(float f) {  // round to nearest even (the default mode)
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// Two signed bytes (bits sh..sh+7 and sh+8..sh+15 of w) -> bf16x2, exactly.
-__device__ inline uint32_t i8x2_bf16(uint32_t w, int sh) {
-    const float a = (float)(int)(int8_t)(w >> sh);
-    const float b = (float)(int)(int8_t)(w >> (sh + 8));
-    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
-}
-
-__device__ inline u32x4 i8x8_bf16(uint32_t lo, uint32_t hi) {
-    return u32x4{i8x2_bf16(lo, 0), i8x2_bf16(lo, 16), i8x2_bf16(hi, 0), i8x2_bf16(hi, 16)};
-}
-
 __device__ inline bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ inline u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
-__device__ inline u32x4 ld16_nt(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
+
+// ---- global -> LDS loads (lane l writes lds + l * size; lds wave-uniform),
+// vmcnt waits and LDS reads as inline asm.  The compiler cannot tell which
+// in-flight global -> LDS load a plain LDS read may alias and would drain
+// them all before it; here each read follows an explicit vmcnt wait for the
+// stage it reads, and each result is tied to an lgkmcnt wait before use.
+__device__ inline void lds_dma16_nt(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 2);  // nontemporal: streamed once
+}
+__device__ inline void lds_dma4(const void *src, void *lds) { __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0); }
+
+template <int N>
+__device__ inline void wait_vmcnt() {  // s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding)
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ inline void wait_vmcnt_le(int n) {  // at most n of this wave's loads outstanding, n <= 10
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        case 7: wait_vmcnt<7>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;
+        default: wait_vmcnt<10>(); break;
+    }
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ inline u32x4 lds_read_b128(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ inline u32x2 lds_read_b64(uint32_t addr) {
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ inline void lds_wait_all(u32x4 &a, u32x4 &b, u32x4 &c, u32x4 &d, u32x2 &e, u32x2 &f, u32x2 &g,
+                                    u32x2 &h) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h));
+}
 
 // ---------------------------------------------------------------------------
 // KV-cache update (attention.hpp:536-652): one wave per sequence, lane l owns
@@ -172,101 +211,67 @@ struct DecArgs {
     int cap, window, ring, odd, keep, rule, n_layers, layer, splits;
 };
 
-// One 16-row block in matrix-instruction operand form.
-struct BlkOp {
-    u32x4 k0, k1;     // key rows: bf16 dims 16g..16g+7, 16g+8..16g+15 of row c
-    u32x2 v[4];       // per dim tile: bf16 values of tokens 4g..4g+3 at dim 16 dt + c
-    float ksc[4];     // key scale * log2(e) / 8 of tokens 4g..4g+3
-    float vsc[4];     // value scale
-};
-
-struct RawI8 {        // an int8 block as loaded
+struct RawI8 {        // an int8 block as loaded: key tile, value tile, scales of tokens 4g..4g+3
     u32x4 k, v;
     u32x2 ks, vs;
 };
 
-__device__ inline void load_i8(const DecArgs &a, size_t kv_base, size_t sc_base, int kvh, int blk,
-                               int c, int g, RawI8 &r) {
-    const size_t t = kv_base + (size_t)(blk * kKvHeads + kvh) * kTile;
-    r.k = ld16_nt(a.kc + t + c * 64 + 16 * g);
-    r.v = ld16_nt(a.vc + t + c * 64 + 16 * g);
-    const size_t s = sc_base + blk * 16 + 4 * g;
-    r.ks = *(const u32x2 *)(a.ks + s);
-    r.vs = *(const u32x2 *)(a.vs + s);
-}
+struct BlkBf {        // a bf16 block (odd layers' kept tokens) in operand form
+    u32x4 k0, k1;     // key row c: dims 16g..16g+7 and 16g+8..16g+15
+    u32x2 v[4];       // per dim tile: tokens 4g..4g+3 at dim 16 dt + c
+};
 
-__device__ inline void op_from_i8(const RawI8 &r, BlkOp &o) {
-    o.k0 = i8x8_bf16(r.k[0], r.k[1]);
-    o.k1 = i8x8_bf16(r.k[2], r.k[3]);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o.v[dt] = u32x2{i8x2_bf16(r.v[dt], 0), i8x2_bf16(r.v[dt], 16)};
-    const float C = 0.125f * kLog2e;
-    o.ksc[0] = h2f(r.ks[0] & 0xffffu) * C;
-    o.ksc[1] = h2f(r.ks[0] >> 16) * C;
-    o.ksc[2] = h2f(r.ks[1] & 0xffffu) * C;
-    o.ksc[3] = h2f(r.ks[1] >> 16) * C;
-    o.vsc[0] = h2f(r.vs[0] & 0xffffu);
-    o.vsc[1] = h2f(r.vs[0] >> 16);
-    o.vsc[2] = h2f(r.vs[1] & 0xffffu);
-    o.vsc[3] = h2f(r.vs[1] >> 16);
-}
-
-__device__ inline void op_from_bf16(const DecArgs &a, size_t slab, int kvh, int blk, int c, int g,
-                                    BlkOp &o) {
-    const size_t t = slab + (size_t)(blk * kKvHeads + kvh) * kTile;
-    o.k0 = ld16(a.kb + t + c * 64 + 16 * g);
-    o.k1 = ld16(a.kb + t + c * 64 + 16 * g + 8);
-    const u32x4 v0 = ld16(a.vb + t + c * 64 + 16 * g);
-    const u32x4 v1 = ld16(a.vb + t + c * 64 + 16 * g + 8);
-    o.v[0] = u32x2{v0[0], v0[1]};
-    o.v[1] = u32x2{v0[2], v0[3]};
-    o.v[2] = u32x2{v1[0], v1[1]};
-    o.v[3] = u32x2{v1[2], v1[3]};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        o.ksc[i] = 0.125f * kLog2e;
-        o.vsc[i] = 1.f;
-    }
-}
-
-__device__ inline void op_zero(BlkOp &o) {
-    o.k0 = o.k1 = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o.v[dt] = u32x2{0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o.ksc[i] = o.vsc[i] = 0.f;
-}
+// One stage of the int8 ring: two blocks' key and value tiles of this
+// wave's KV head, and their scales (lane-ordered as the loads write them).
+constexpr int kStages = 3;
+struct AttnStage {
+    u32x4 k[2][64];
+    u32x4 v[2][64];
+    uint32_t sc[64];
+};
 
 struct SoftState {
     float m, l;       // running max (log2 domain) and this lane's part of the sum, for head c
     f32x4 o[4];       // O[head 4g+i][dim 16 dt + c]
 };
 
-// Two blocks (32 tokens) starting at block `blk`; `nb` of them present (1 or 2).
-// Rows at or past `nvalid` weigh nothing.  `zero_v` clears value elements of
-// such rows (bf16 rows past the written ones may hold anything).
-__device__ inline void pair_step(const BlkOp &A, const BlkOp &B, int blk, int nb, int nvalid, int g,
-                                 int lane, bf16x8 q0, bf16x8 q1, bool zero_v, SoftState &st) {
-    f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A.k0), q0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A.k1), q1, s0, 0, 0, 0);
-    f32x4 s1 = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (nb > 1) {
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(B.k0), q0, s1, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(B.k1), q1, s1, 0, 0, 0);
-    }
-    float sv[8];
-    bool ok[8];
-    const int row0 = blk * 16 + 4 * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ok[i] = row0 + i < nvalid;
-        ok[4 + i] = nb > 1 && row0 + 16 + i < nvalid;
-        sv[i] = ok[i] ? s0[i] * A.ksc[i] : -INFINITY;
-        sv[4 + i] = ok[4 + i] ? s1[i] * B.ksc[i] : -INFINITY;
-    }
-    float bm = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) bm = fmaxf(bm, sv[j]);
+__device__ inline void load_bf(const DecArgs &a, size_t slab, int kvh, int blk, int c, int g, BlkBf &o) {
+    const size_t t = slab + (size_t)(blk * kKvHeads + kvh) * kTile + c * 64 + 16 * g;
+    o.k0 = ld16(a.kb + t);
+    o.k1 = ld16(a.kb + t + 8);
+    const u32x4 v0 = ld16(a.vb + t), v1 = ld16(a.vb + t + 8);
+    o.v[0] = u32x2{v0[0], v0[1]};
+    o.v[1] = u32x2{v0[2], v0[3]};
+    o.v[2] = u32x2{v1[0], v1[1]};
+    o.v[3] = u32x2{v1[2], v1[3]};
+}
+
+__device__ inline uint32_t pk_bf16(float a, float b) {  // two floats -> bf16x2, nearest even
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// Four signed bytes -> four bf16 (exact).
+__device__ inline u32x2 i8x4_bf16(uint32_t w) {
+    return u32x2{pk_bf16((float)(int8_t)w, (float)(int8_t)(w >> 8)),
+                 pk_bf16((float)(int8_t)(w >> 16), (float)(int8_t)(w >> 24))};
+}
+
+__device__ inline void unpack_h4(u32x2 h, float mul, float *out) {  // four fp16 -> float * mul
+    out[0] = h2f(h[0] & 0xffffu) * mul;
+    out[1] = h2f(h[0] >> 16) * mul;
+    out[2] = h2f(h[1] & 0xffffu) * mul;
+    out[3] = h2f(h[1] >> 16) * mul;
+}
+
+// Online-softmax update and O += P'.V for 32 tokens.  sv: scores (log2
+// domain; -inf where masked); vsc(j): value scale of token slot j (0 where
+// masked); vop(dt): the value operand of dim tile dt (tokens of the first
+// block, then the second).  Both are called where their results are used,
+// which keeps them out of the registers live across the softmax.
+template <class VScale, class VOp>
+__device__ inline void softmax_pv(const float (&sv)[8], VScale vsc, VOp vop, int g, SoftState &st) {
+    float bm = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                     fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
     bm = fmaxf(bm, __shfl_xor(bm, 16));
     bm = fmaxf(bm, __shfl_xor(bm, 32));
     const float mn = fmaxf(st.m, bm);
@@ -279,39 +284,110 @@ __device__ inline void pair_step(const BlkOp &A, const BlkOp &B, int blk, int nb
     }
     st.l = st.l * alpha + ps;
     st.m = mn;
-    uint32_t pw[4];
+    const bf16x8 pop = __builtin_bit_cast(
+        bf16x8, u32x4{pk_bf16(p[0] * vsc(0), p[1] * vsc(1)), pk_bf16(p[2] * vsc(2), p[3] * vsc(3)),
+                      pk_bf16(p[4] * vsc(4), p[5] * vsc(5)), pk_bf16(p[6] * vsc(6), p[7] * vsc(7))});
+    // rescale the output rows only when some head's maximum moved (alpha != 1)
+    if (__ballot(alpha != 1.f)) {
+        float ar[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float lo = ok[2 * j] ? p[2 * j] * (j < 2 ? A.vsc[2 * j] : B.vsc[2 * j - 4]) : 0.f;
-        const float hi = ok[2 * j + 1] ? p[2 * j + 1] * (j < 2 ? A.vsc[2 * j + 1] : B.vsc[2 * j - 3]) : 0.f;
-        pw[j] = f2bf(lo) | (f2bf(hi) << 16);
+        for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st.o[dt][i] *= ar[i];
     }
-    const bf16x8 pop = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
-    float ar[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
-    (void)lane;
+    for (int dt = 0; dt < 4; ++dt)
+        st.o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, as_bf16x8(vop(dt)), st.o[dt], 0, 0, 0);
+}
+
+// Scores of one int8 key tile: the query as Q = 256 hi + lo (int8 each),
+// exact in int32.
+__device__ inline i32x4 qk_i8(u32x4 k, i32x4 qh, i32x4 ql) {
+    const i32x4 kk = __builtin_bit_cast(i32x4, k);
+    i32x4 s = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, qh, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    s = s << 8;
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, ql, s, 0, 0, 0);
+}
+
+// Two int8 blocks (32 tokens) from block `blk`, `nb` (1 or 2) present.
+// kMask: some row is at or past `nvalid` (else every row counts).
+template <bool kMask>
+__device__ inline void pair_i8(const RawI8 &A, const RawI8 &B, int blk, int nb, int nvalid, int g,
+                               i32x4 qh, i32x4 ql, float qf, SoftState &st) {
+    const i32x4 sa = qk_i8(A.k, qh, ql);
+    const i32x4 sb = (!kMask || nb > 1) ? qk_i8(B.k, qh, ql) : i32x4{0, 0, 0, 0};
+    float sv[8];
+    {
+        float ksc[8];
+        unpack_h4(A.ks, qf, ksc);
+        unpack_h4(B.ks, qf, ksc + 4);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-        u32x2 va = A.v[dt], vb = nb > 1 ? B.v[dt] : u32x2{0u, 0u};
-        if (zero_v) {
-            va[0] &= (ok[0] ? 0xffffu : 0u) | (ok[1] ? 0xffff0000u : 0u);
-            va[1] &= (ok[2] ? 0xffffu : 0u) | (ok[3] ? 0xffff0000u : 0u);
-            vb[0] &= (ok[4] ? 0xffffu : 0u) | (ok[5] ? 0xffff0000u : 0u);
-            vb[1] &= (ok[6] ? 0xffffu : 0u) | (ok[7] ? 0xffff0000u : 0u);
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = (float)sa[i] * ksc[i];
+            sv[4 + i] = (float)sb[i] * ksc[4 + i];
         }
-        f32x4 acc = st.o[dt];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] *= ar[i];
-        st.o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, as_bf16x8(u32x4{va[0], va[1], vb[0], vb[1]}),
-                                                          acc, 0, 0, 0);
     }
+    const int row0 = blk * 16 + 4 * g;
+    if (kMask) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = row0 + i < nvalid ? sv[i] : -INFINITY;
+            sv[4 + i] = nb > 1 && row0 + 16 + i < nvalid ? sv[4 + i] : -INFINITY;
+        }
+    }
+    auto vsc = [&](int j) {
+        const u32x2 h = j < 4 ? A.vs : B.vs;
+        const float v = h2f((j & 2 ? h[1] : h[0]) >> (j & 1 ? 16 : 0) & 0xffffu);
+        if (!kMask) return v;
+        const bool ok = j < 4 ? row0 + j < nvalid : (nb > 1 && row0 + 12 + j < nvalid);
+        return ok ? v : 0.f;
+    };
+    auto vop = [&](int dt) {
+        const u32x2 x = i8x4_bf16(A.v[dt]), y = i8x4_bf16(B.v[dt]);
+        return u32x4{x[0], x[1], y[0], y[1]};
+    };
+    softmax_pv(sv, vsc, vop, g, st);
+}
+
+// Two bf16 blocks from block `blk` (`nb` present); values of masked rows
+// are cleared, since rows past the written ones may hold anything.
+__device__ inline void pair_bf(const BlkBf &A, const BlkBf &B, int blk, int nb, int nvalid, int g,
+                               bf16x8 q0, bf16x8 q1, SoftState &st) {
+    const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A.k0), q0, z, 0, 0, 0);
+    sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(A.k1), q1, sa, 0, 0, 0);
+    f32x4 sb = z;
+    if (nb > 1) {
+        sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(B.k0), q0, z, 0, 0, 0);
+        sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(B.k1), q1, sb, 0, 0, 0);
+    }
+    const float C = 0.125f * kLog2e;
+    const int row0 = blk * 16 + 4 * g;
+    float sv[8];
+    uint32_t keep[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sv[i] = row0 + i < nvalid ? sa[i] * C : -INFINITY;
+        sv[4 + i] = nb > 1 && row0 + 16 + i < nvalid ? sb[i] * C : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        keep[j] = (sv[2 * j] != -INFINITY ? 0xffffu : 0u) | (sv[2 * j + 1] != -INFINITY ? 0xffff0000u : 0u);
+    auto vsc = [&](int j) { return sv[j] != -INFINITY ? 1.f : 0.f; };
+    auto vop = [&](int dt) {
+        const u32x2 y = nb > 1 ? B.v[dt] : u32x2{0u, 0u};
+        return u32x4{A.v[dt][0] & keep[0], A.v[dt][1] & keep[1], y[0] & keep[2], y[1] & keep[3]};
+    };
+    softmax_pv(sv, vsc, vop, g, st);
 }
 
 __device__ inline bool seq_valid(const DecArgs &a, int pos) { return pos >= 0 && (a.ring || pos < a.cap); }
 
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void attn_decode_kernel(DecArgs a) {
-    __shared__ float red[kGqa * kHd];
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3, 8))) void attn_decode_kernel(DecArgs a) {
+    __shared__ AttnStage ring[kStages];
+    float *red = reinterpret_cast<float *>(&ring[0]);  // after the loop: the output rows
     const int S = a.splits;
     const int s = blockIdx.x % S;
     const int bk = blockIdx.x / S;
@@ -330,12 +406,42 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                                                                          : min(nblk, a.keep >> 4);
     const int blk0 = (int)((int64_t)nblk * s / S), blk1 = (int)((int64_t)nblk * (s + 1) / S);
 
-    bf16x8 q0 = as_bf16x8(u32x4{0u, 0u, 0u, 0u}), q1 = q0;
+    // The query of head c (heads 8..15 of the instruction are zero), dims
+    // 16g..16g+15: as bf16 for the kept blocks, and as Q = rint(q 2^E) =
+    // 256 hi + lo with |Q| < 2^14 (E per head) for the int8 blocks.
+    u32x4 qa = u32x4{0u, 0u, 0u, 0u}, qb = qa;
     if (c < kGqa) {
         const uint16_t *qp = a.q + ((size_t)b * kKvHeads * kGqa + kvh * kGqa + c) * kHd + 16 * g;
-        q0 = as_bf16x8(ld16(qp));
-        q1 = as_bf16x8(ld16(qp + 8));
+        qa = ld16(qp);
+        qb = ld16(qp + 8);
     }
+    const bf16x8 q0 = as_bf16x8(qa), q1 = as_bf16x8(qb);
+    float qv[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        qv[2 * j] = bf2f(qa[j] & 0xffffu);
+        qv[2 * j + 1] = bf2f(qa[j] >> 16);
+        qv[8 + 2 * j] = bf2f(qb[j] & 0xffffu);
+        qv[8 + 2 * j + 1] = bf2f(qb[j] >> 16);
+    }
+    float qm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) qm = fmaxf(qm, fabsf(qv[j]));
+    qm = fmaxf(qm, __shfl_xor(qm, 16));
+    qm = fmaxf(qm, __shfl_xor(qm, 32));
+    const int E = 14 - __builtin_amdgcn_frexp_expf(qm);  // qm 2^E in [2^13, 2^14)
+    uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int Q = (int)__builtin_rintf(__builtin_ldexpf(qv[j], E));
+        const int hi = (Q + 128) >> 8, lo = Q - (hi << 8);
+        hw[j >> 2] |= (uint32_t)(uint8_t)hi << (8 * (j & 3));
+        lw[j >> 2] |= (uint32_t)(uint8_t)lo << (8 * (j & 3));
+    }
+    const i32x4 qh = __builtin_bit_cast(i32x4, u32x4{hw[0], hw[1], hw[2], hw[3]});
+    const i32x4 ql = __builtin_bit_cast(i32x4, u32x4{lw[0], lw[1], lw[2], lw[3]});
+    const float qf = __builtin_ldexpf(0.125f * kLog2e, -E);
+
     SoftState st;
     st.m = -INFINITY;
     st.l = 0.f;
@@ -348,30 +454,68 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const size_t slab = ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
         for (int blk = blk0; blk < e16; blk += 2) {
             const int nb = min(2, e16 - blk);
-            BlkOp A, B;
-            op_from_bf16(a, slab, kvh, blk, c, g, A);
-            if (nb > 1) op_from_bf16(a, slab, kvh, blk + 1, c, g, B);
-            else op_zero(B);
-            pair_step(A, B, blk, nb, nvalid, g, lane, q0, q1, true, st);
+            BlkBf A, B;
+            load_bf(a, slab, kvh, blk, c, g, A);
+            if (nb > 1) load_bf(a, slab, kvh, blk + 1, c, g, B);
+            else B = A;  // not used: its rows are masked
+            pair_bf(A, B, blk, nb, nvalid, g, q0, q1, st);
         }
     }
     const int i0 = max(blk0, nb16);
     if (i0 < blk1) {
-        const size_t kv_base = (size_t)b * a.bks + a.lko;
-        const size_t sc_base = (size_t)b * a.bss + a.lso;
-        RawI8 nA, nB;
-        load_i8(a, kv_base, sc_base, kvh, i0, c, g, nA);
-        if (i0 + 1 < blk1) load_i8(a, kv_base, sc_base, kvh, i0 + 1, c, g, nB);
-        for (int blk = i0; blk < blk1; blk += 2) {
-            const int nb = min(2, blk1 - blk);
-            const RawI8 rA = nA, rB = nB;
-            if (blk + 2 < blk1) load_i8(a, kv_base, sc_base, kvh, blk + 2, c, g, nA);
-            if (blk + 3 < blk1) load_i8(a, kv_base, sc_base, kvh, blk + 3, c, g, nB);
-            BlkOp A, B;
-            op_from_i8(rA, A);
-            if (nb > 1) op_from_i8(rB, B);
-            else op_zero(B);
-            pair_step(A, B, blk, nb, nvalid, g, lane, q0, q1, false, st);
+        // int8 blocks, two per stage, through a ring of kStages LDS slots:
+        // stage p (blocks i0 + 2p, +1) lands while earlier stages compute.
+        const char *kb = reinterpret_cast<const char *>(a.kc + (size_t)b * a.bks + a.lko) + kvh * kTile;
+        const char *vb = reinterpret_cast<const char *>(a.vc + (size_t)b * a.bks + a.lko) + kvh * kTile;
+        const char *ksb = reinterpret_cast<const char *>(a.ks + (size_t)b * a.bss + a.lso);
+        const char *vsb = reinterpret_cast<const char *>(a.vs + (size_t)b * a.bss + a.lso);
+        const int npairs = (blk1 - i0 + 1) >> 1;
+        const int last = i0 + 2 * (npairs - 1);
+        const int nfull = (blk1 - last == 2 && (last + 2) * 16 <= nvalid) ? npairs : npairs - 1;
+        // scale lanes: 0..7 key scales of the first block, 8..15 of the second,
+        // 16..23 / 24..31 value scales; lanes 32..63 repeat 0..31
+        const int sl = lane & 31;
+        const char *sbase = (sl < 16 ? ksb : vsb) + (sl & 7) * 4;
+        const int sblk = (sl >> 3) & 1;
+        auto loads = [&](int p) { return i0 + 2 * p + 1 < blk1 ? 5 : 3; };  // global -> LDS loads of stage p
+        auto issue = [&](int p) {
+            AttnStage &sg = ring[p % kStages];
+            const int blk = i0 + 2 * p;
+            const bool two = blk + 1 < blk1;
+            const size_t t0 = (size_t)blk * kKvHeads * kTile;
+            const size_t t1 = t0 + (two ? (size_t)kKvHeads * kTile : 0);
+            lds_dma16_nt(kb + t0 + 16 * lane, &sg.k[0][0]);
+            lds_dma16_nt(vb + t0 + 16 * lane, &sg.v[0][0]);
+            if (two) {
+                lds_dma16_nt(kb + t1 + 16 * lane, &sg.k[1][0]);
+                lds_dma16_nt(vb + t1 + 16 * lane, &sg.v[1][0]);
+            }
+            lds_dma4(sbase + (size_t)(blk + (two ? sblk : 0)) * 32, &sg.sc[0]);
+        };
+        for (int p = 0; p < min(kStages - 1, npairs); ++p) issue(p);
+        for (int p = 0; p < npairs; ++p) {
+            if (p + kStages - 1 < npairs) issue(p + kStages - 1);
+            // loads of the stages after p may stay in flight
+            int after = 0;
+            for (int q = p + 1; q < min(p + kStages, npairs); ++q) after += loads(q);
+            wait_vmcnt_le(after);
+            const AttnStage &sg = ring[p % kStages];
+            const uint32_t ka = lds_addr(&sg.k[0][0]) + c * 64 + 16 * g;
+            RawI8 A, B;
+            A.k = lds_read_b128(ka);
+            A.v = lds_read_b128(ka + (uint32_t)(offsetof(AttnStage, v) - offsetof(AttnStage, k)));
+            B.k = lds_read_b128(ka + 1024u);
+            B.v = lds_read_b128(ka + 1024u + (uint32_t)(offsetof(AttnStage, v) - offsetof(AttnStage, k)));
+            const uint32_t sa = lds_addr(&sg.sc[0]) + 8 * g;
+            A.ks = lds_read_b64(sa);
+            B.ks = lds_read_b64(sa + 32);
+            A.vs = lds_read_b64(sa + 64);
+            B.vs = lds_read_b64(sa + 96);
+            lds_wait_all(A.k, A.v, B.k, B.v, A.ks, B.ks, A.vs, B.vs);
+            asm volatile("" ::: "memory");  // the slot is free for a later stage's loads
+            const int blk = i0 + 2 * p;
+            if (p < nfull) pair_i8<false>(A, B, blk, 2, nvalid, g, qh, ql, qf, st);
+            else pair_i8<true>(A, B, blk, min(2, blk1 - blk), nvalid, g, qh, ql, qf, st);
         }
     }
 
@@ -396,7 +540,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         __syncthreads();
         uint32_t w[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = f2bf(red[8 * lane + 2 * j]) | (f2bf(red[8 * lane + 2 * j + 1]) << 16);
+        for (int j = 0; j < 4; ++j) w[j] = pk_bf16(red[8 * lane + 2 * j], red[8 * lane + 2 * j + 1]);
         *(u32x4 *)(out + 8 * lane) = u32x4{w[0], w[1], w[2], w[3]};
     } else {
         float *part = a.ws + ((size_t)bk * S + s) * kPartFloats;
@@ -448,7 +592,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(DecArgs a) {
     const float f = al / (L * al + __builtin_amdgcn_exp2f(sk - mf));
     uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = f2bf(o[2 * j] * f) | (f2bf(o[2 * j + 1] * f) << 16);
+    for (int j = 0; j < 4; ++j) w[j] = pk_bf16(o[2 * j] * f, o[2 * j + 1] * f);
     *(u32x4 *)out = u32x4{w[0], w[1], w[2], w[3]};
 }
 

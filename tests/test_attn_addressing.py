@@ -41,17 +41,37 @@ def test_kv_update_lane_stores_match_layout():
 
 
 def mfma(a_lanes, b_lanes, acc):
-    """v_mfma_f32_16x16x32_bf16 on per-lane operands [64][8] (fp32 values)."""
-    A = np.zeros((16, 32), np.float64)
-    B = np.zeros((32, 16), np.float64)
+    """A 16x16 matrix instruction on per-lane operands [64][kpl] (values as
+    floats): v_mfma_f32_16x16x32_bf16 (kpl 8) or v_mfma_i32_16x16x64_i8
+    (kpl 16, integer values, exact in float64)."""
+    kpl = a_lanes.shape[1]
+    A = np.zeros((16, 4 * kpl), np.float64)
+    B = np.zeros((4 * kpl, 16), np.float64)
     for l in range(64):
-        A[l % 16, 8 * (l // 16):8 * (l // 16) + 8] = a_lanes[l]
-        B[8 * (l // 16):8 * (l // 16) + 8, l % 16] = b_lanes[l]
+        A[l % 16, kpl * (l // 16):kpl * (l // 16) + kpl] = a_lanes[l]
+        B[kpl * (l // 16):kpl * (l // 16) + kpl, l % 16] = b_lanes[l]
     D = A @ B
     out = acc.astype(np.float64).copy()
     for l in range(64):
         out[l] += D[4 * (l // 16):4 * (l // 16) + 4, l % 16]
-    return out.astype(np.float32)
+    return out
+
+
+def split_query(qf_lanes):
+    """The decode kernel's int8 query: per head (lane column), E = 14 -
+    frexp exponent of the head's max |q|, Q = rint(q 2^E) = 256 hi + lo.
+    Returns hi, lo [64][16] and 2^-E log2(e) / 8 per lane."""
+    qm = np.abs(qf_lanes).max(1)
+    qm = np.maximum(qm, qm[LANE ^ 16])
+    qm = np.maximum(qm, qm[LANE ^ 32])
+    E = 14 - np.frexp(qm)[1]
+    Q = np.rint(np.ldexp(qf_lanes.astype(np.float64), E[:, None])).astype(np.int64)
+    hi = (Q + 128) >> 8
+    lo = Q - (hi << 8)
+    assert np.abs(Q).max() <= 1 << 14
+    assert hi.min() >= -128 and hi.max() <= 127 and lo.min() >= -128 and lo.max() <= 127
+    qf = np.ldexp(np.float32(0.125) * LOG2E, -E).astype(np.float32)
+    return hi.astype(np.float64), lo.astype(np.float64), qf
 
 
 def bf16r(x):
@@ -87,13 +107,14 @@ def decode_mirror(c, S, rule, slabs):
                     if m[l]:
                         qv[l] = qf[heads[l], 16 * G[l]:16 * G[l] + 16]
                 q0, q1 = qv[:, :8], qv[:, 8:]
+                qhi, qlo, qfac = split_query(qv)
                 M = np.full(64, -np.inf, np.float32)
                 Ls = np.zeros(64, np.float32)
                 O = np.zeros((4, 64, 4), np.float32)
 
-                def block_ops(blk, bf16):
-                    if blk is None:
-                        return None
+                def block_ops(pair_blk, bf16, two, sub):
+                    """Operands of block pair_blk + sub of the pair at pair_blk."""
+                    blk = pair_blk + sub
                     t = (blk * N_KV + kvh) * TILE
                     if bf16:
                         ko = t + C * 64 + 16 * G
@@ -107,20 +128,39 @@ def decode_mirror(c, S, rule, slabs):
                         assert ko.max() + 16 <= slab_k.size
                         kk = np.stack([slab_k[o:o + 16] for o in ko]).astype(np.float32)
                         vv = np.stack([slab_v[o:o + 16] for o in ko]).astype(np.float32)
-                        so = blk * 16 + 4 * G
-                        assert so.max() + 4 <= c.cap
-                        ksc = np.stack([ksf[o:o + 4] for o in so]) * (np.float32(0.125) * LOG2E)
-                        vsc = np.stack([vsf[o:o + 4] for o in so])
+                        # scales through the stage's scale lanes: lane sl < 32 loads
+                        # 4 B of (key if sl < 16 else value) scales of block
+                        # blk + ((sl >> 3) & 1) at byte (sl & 7) * 4
+                        sl = np.arange(32)
+                        src_blk = pair_blk + ((sl >> 3) & 1) if two else np.full(32, pair_blk)
+                        src = src_blk * 16 + (sl & 7) * 2          # first half of the 4 bytes
+                        assert src.max() + 2 <= c.cap
+                        stage = np.where(sl[:, None] < 16, ksf[np.stack([src, src + 1], 1)],
+                                         vsf[np.stack([src, src + 1], 1)]).ravel()
+                        # lane (c, g) reads 8 B at 8g (+32 second block, +64 values)
+                        half = (32 if sub else 0)
+                        ks_l = np.stack([stage[(half + 8 * g) // 2:(half + 8 * g) // 2 + 4] for g in G])
+                        vs_l = np.stack([stage[(64 + half + 8 * g) // 2:(64 + half + 8 * g) // 2 + 4] for g in G])
+                        ksc = ks_l * qfac[:, None]
+                        vsc = vs_l
                     # value operand per dim tile: elements dt * 4 + i
                     vop = [vv[:, 4 * dt:4 * dt + 4] for dt in range(4)]
                     return kk[:, :8], kk[:, 8:], vop, ksc.astype(np.float32), vsc.astype(np.float32)
 
                 def step(blk, nb, bf16):
                     nonlocal M, Ls, O
-                    A = block_ops(blk, bf16)
-                    Bo = block_ops(blk + 1, bf16) if nb > 1 else None
-                    s0 = mfma(A[1], q1, mfma(A[0], q0, np.zeros((64, 4), np.float32)))
-                    s1 = mfma(Bo[1], q1, mfma(Bo[0], q0, np.zeros((64, 4), np.float32))) if Bo else np.zeros((64, 4), np.float32)
+                    A = block_ops(blk, bf16, nb > 1, 0)
+                    Bo = block_ops(blk, bf16, True, 1) if nb > 1 else None
+
+                    def scores(X):
+                        if bf16:
+                            return mfma(X[1], q1, mfma(X[0], q0, np.zeros((64, 4)))).astype(np.float32)
+                        kk = np.concatenate([X[0], X[1]], 1)        # the tile's 16 raw bytes
+                        si = mfma(kk, qhi, np.zeros((64, 4))) * 256 + mfma(kk, qlo, np.zeros((64, 4)))
+                        assert np.abs(si).max() < 2 ** 31
+                        return si.astype(np.float32)                # int32 -> float, nearest
+                    s0 = scores(A)
+                    s1 = scores(Bo) if Bo else np.zeros((64, 4), np.float32)
                     row0 = blk * 16 + 4 * G
                     ok = np.zeros((64, 8), bool)
                     sv = np.full((64, 8), -np.inf, np.float32)
@@ -147,7 +187,7 @@ def decode_mirror(c, S, rule, slabs):
                         vop = np.concatenate([va, vb], 1)
                         if bf16:
                             vop = np.where(ok, vop, 0)
-                        O[dt] = mfma(pop, vop, O[dt] * ar)
+                        O[dt] = mfma(pop, vop, O[dt] * ar).astype(np.float32)
 
                 e16 = min(blk1, nb16)
                 for blk in range(blk0, e16, 2):
