@@ -269,3 +269,120 @@ int orc_attn_decode(int B, int n_heads, int n_kv_heads, int head_dim, int cap, i
     }
     return bad ? -1 : 0;
 }
+
+/* ------------------------------------------------- decoder-step pieces -- */
+
+/* RoPE tables with YaRN (compute_concentration_and_inv_freq and
+ * compute_cos_sin, run.cpp:422-503; the reference GPU path fills its
+ * cos/sin tables on the host with them, getp_run.cpp:1876-1890):
+ * cos_out/sin_out [n_pos][head_dim / 2].  ntk_beta 32, ntk_alpha 1
+ * (run.cpp:576-577).  Returns -1 where run.cpp's assert would fail. */
+int orc_rope_table(float base, int head_dim, float scaling_factor, float initial_context_length,
+                   int n_pos, float *cos_out, float *sin_out) {
+    const int d_half = head_dim / 2;
+    const float ntk_beta = 32.0f, ntk_alpha = 1.0f;
+    float inv_freq[512];
+    if (d_half > 512) return -1;
+    float concentration = 1.0f;
+    if (scaling_factor > 1.0f) {
+        concentration = 0.1f * logf(scaling_factor) + 1.0f;
+        /* M_PI is a double there: the quotient is taken in double and
+         * rounded to float by logf's parameter */
+        const double pi = 3.14159265358979323846;
+        const float low = d_half * logf((float)(initial_context_length / (ntk_beta * 2.0f * pi))) / logf(base);
+        const float high = d_half * logf((float)(initial_context_length / (ntk_alpha * 2.0f * pi))) / logf(base);
+        if (!(0 < low && low < high && high < d_half - 1)) return -1;
+        for (int i = 0; i < d_half; i++) {
+            const float freq = powf(base, ((float)(2 * i)) / (float)head_dim);
+            const float interpolation = 1.0f / (scaling_factor * freq);
+            const float extrapolation = 1.0f / freq;
+            float ramp = ((float)i - low) / (high - low);
+            if (ramp < 0) ramp = 0;
+            if (ramp > 1) ramp = 1;
+            const float mask = 1.0f - ramp;
+            inv_freq[i] = interpolation * (1.0f - mask) + extrapolation * mask;
+        }
+    } else {
+        for (int i = 0; i < d_half; i++) inv_freq[i] = 1.0f / powf(base, ((float)(2 * i)) / (float)head_dim);
+    }
+    for (int p = 0; p < n_pos; ++p)
+        for (int j = 0; j < d_half; j++) {
+            const float val = (float)p * inv_freq[j];
+            cos_out[(size_t)p * d_half + j] = cosf(val) * concentration;
+            sin_out[(size_t)p * d_half + j] = sinf(val) * concentration;
+        }
+    return 0;
+}
+
+/* Bias add + split + RoPE of the QKV projection (add_bias_kernel,
+ * other_kernels.hpp:53-61, then split_qkv_apply_rotary_kernel_vec_bf16,
+ * rope.hpp:209-330): qkv bf16 [B][(nq + 2 nkv) hd] (the GEMM output,
+ * already bf16), bias bf16; each element first bf16(x + b); then for head
+ * element pairs (i, i + hd/2) at position pos: y0 = a c - b s,
+ * y1 = b c + a s in fp32, rounded to bf16.  The fp32 rotation is evaluated
+ * as fmaf(a, c, -(b * s)) and fmaf(b, c, a * s) (the reference leaves the
+ * contraction to its compiler).  v is copied. */
+void orc_qkv_bias_rope(const uint16_t *qkv, const uint16_t *bias, const float *cos_t,
+                       const float *sin_t, const int32_t *pos, int B, int nq, int nkv, int hd,
+                       uint16_t *q, uint16_t *k, uint16_t *v) {
+    const int width = (nq + 2 * nkv) * hd, half = hd / 2;
+    for (int b = 0; b < B; ++b) {
+        const uint16_t *row = qkv + (size_t)b * width;
+        const float *cs = cos_t + (size_t)pos[b] * half, *sn = sin_t + (size_t)pos[b] * half;
+        for (int h = 0; h < nq + nkv; ++h) {
+            uint16_t *dst = h < nq ? q + ((size_t)b * nq + h) * hd : k + ((size_t)b * nkv + h - nq) * hd;
+            for (int i = 0; i < half; ++i) {
+                const int e0 = h * hd + i, e1 = e0 + half;
+                const float a = orc_bf2f(orc_f2bf(orc_bf2f(row[e0]) + orc_bf2f(bias[e0])));
+                const float c2 = orc_bf2f(orc_f2bf(orc_bf2f(row[e1]) + orc_bf2f(bias[e1])));
+                dst[i] = orc_f2bf(fmaf(a, cs[i], -(c2 * sn[i])));
+                dst[i + half] = orc_f2bf(fmaf(c2, cs[i], a * sn[i]));
+            }
+        }
+        for (int i = 0; i < nkv * hd; ++i) {
+            const int e = (nq + nkv) * hd + i;
+            v[(size_t)b * nkv * hd + i] = orc_f2bf(orc_bf2f(row[e]) + orc_bf2f(bias[e]));
+        }
+    }
+}
+
+/* Output projection epilogue (store_and_fuse_tile_bf16, matmul.hpp:121-139):
+ * x = bf16(bf16(proj + bias) + x), proj the GEMM output already in bf16. */
+void orc_bias_residual(uint16_t *x, const uint16_t *proj, const uint16_t *bias, int B, int H) {
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H; ++h) {
+            const size_t i = (size_t)b * H + h;
+            const float v = orc_bf2f(orc_f2bf(orc_bf2f(proj[i]) + orc_bf2f(bias[h])));
+            x[i] = orc_f2bf(v + orc_bf2f(x[i]));
+        }
+}
+
+/* Dense bf16 GEMM out[m][n] = bf16(sum_k a[m][k] w[n][k]) with a double
+ * accumulator (the limit of any fp32 MFMA order). */
+void orc_matmul_bf16(const uint16_t *a, const uint16_t *w, int M, int N, int K, uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double acc = 0.0;
+            const uint16_t *ar = a + (size_t)m * K, *wr = w + (size_t)n * K;
+            for (int k = 0; k < K; ++k) acc += (double)orc_bf2f(ar[k]) * (double)orc_bf2f(wr[k]);
+            out[(size_t)m * N + n] = orc_f2bf((float)acc);
+        }
+}
+
+/* Greedy sampling (sample_argmax_kernel_bf16, softmax.hpp:236-290): the
+ * first index of the largest bf16 value of each row. */
+void orc_argmax_bf16(const uint16_t *logits, int B, int n, int32_t *out) {
+    for (int b = 0; b < B; ++b) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int i = 0; i < n; ++i) {
+            const float p = orc_bf2f(logits[(size_t)b * n + i]);
+            if (p > best || (p == best && i < bi)) {
+                best = p;
+                bi = i;
+            }
+        }
+        out[b] = bi;
+    }
+}

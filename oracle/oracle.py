@@ -47,6 +47,11 @@ _SIGS = {
     "orc_kv_quantize_row": (None, [_P, _I, _P, _P]),
     "orc_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                              _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "orc_rope_table": (_I, [_F, _I, _F, _F, _I, _P, _P]),
+    "orc_qkv_bias_rope": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
+    "orc_bias_residual": (None, [_P, _P, _P, _I, _I]),
+    "orc_matmul_bf16": (None, [_P, _P, _I, _I, _I, _P]),
+    "orc_argmax_bf16": (None, [_P, _I, _I, _P]),
 }
 
 _lib = None
@@ -301,4 +306,47 @@ def attn_decode(q, kq, vq, ks, vs, kb, vb, sinks, pos, *, n_kv_heads: int, layer
                                _p(kb), _p(vb), _p(sinks), _p(pos), _p(out))
     if rc != 0:
         raise ValueError("orc_attn_decode: shape outside the restatement")
+    return out
+
+
+def rope_table(n_pos: int, base=150000.0, head_dim=64, scaling=32.0, init_ctx=4096.0):
+    """cos, sin fp32 [n_pos][head_dim / 2] (run.cpp:422-503); gpt-oss
+    defaults: rope_theta 150000, scaling factor 32, initial context 4096."""
+    c = np.empty((n_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    if lib().orc_rope_table(base, head_dim, scaling, init_ctx, n_pos, _p(c), _p(s)) != 0:
+        raise ValueError("rope parameters fail run.cpp's assertion")
+    return c, s
+
+
+def qkv_bias_rope(qkv, bias, cos, sin, pos, nq=64, nkv=8, hd=64):
+    qkv, bias = _c(qkv, np.uint16), _c(bias, np.uint16)
+    cos, sin, pos = _c(cos, np.float32), _c(sin, np.float32), _c(pos, np.int32)
+    B = qkv.shape[0]
+    q = np.empty((B, nq, hd), np.uint16)
+    k = np.empty((B, nkv * hd), np.uint16)
+    v = np.empty((B, nkv * hd), np.uint16)
+    lib().orc_qkv_bias_rope(_p(qkv), _p(bias), _p(cos), _p(sin), _p(pos), B, nq, nkv, hd, _p(q),
+                            _p(k), _p(v))
+    return q, k, v
+
+
+def bias_residual(x, proj, bias):
+    x = np.array(x, np.uint16, copy=True, order="C")
+    proj, bias = _c(proj, np.uint16), _c(bias, np.uint16)
+    lib().orc_bias_residual(_p(x), _p(proj), _p(bias), x.shape[0], x.shape[1])
+    return x
+
+
+def matmul_bf16(a, w):
+    a, w = _c(a, np.uint16), _c(w, np.uint16)
+    out = np.empty((a.shape[0], w.shape[0]), np.uint16)
+    lib().orc_matmul_bf16(_p(a), _p(w), a.shape[0], w.shape[0], a.shape[1], _p(out))
+    return out
+
+
+def argmax_bf16(logits):
+    logits = _c(logits, np.uint16)
+    out = np.empty(logits.shape[0], np.int32)
+    lib().orc_argmax_bf16(_p(logits), logits.shape[0], logits.shape[1], _p(out))
     return out
