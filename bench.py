@@ -42,6 +42,8 @@ def parse():
                     help="skip the C4 MoE-share and attention lines (24 layers at 512 tokens)")
     ap.add_argument("--attn-only", action="store_true",
                     help="only the C4 attention line (decode attention over the int8 KV cache)")
+    ap.add_argument("--decoder-only", action="store_true",
+                    help="only the C4 decode-step line (24 layers, 512 sequences)")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -347,6 +349,49 @@ def time_c4_attention(args, dev):
             "hbm_frac_odd_layer": round(b_odd / (ms_odd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def time_c4_decoder(args, dev):
+    """Config C4 end to end: one decode step of the 20B-shape decoder (24
+    layers, vocabulary 201088) for 512 sequences at position 1023, random
+    weights generated on the device (MoE layers packed), KV caches filled
+    with random rows for positions 0..1022.  The dense projections run on
+    the platform GEMM (torch.matmul); attention, MoE and the glue on this
+    package's kernels.  An extra line, not `value`."""
+    import torch
+    import decoder as dec
+    cfg = dec.DecoderConfig()
+    B = 512
+    model = dec.random_on_device(cfg, B, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0xC4C4)
+    pool = [(torch.randn((B, 512), generator=g, device=dev).to(torch.bfloat16),
+             torch.randn((B, 512), generator=g, device=dev).to(torch.bfloat16)) for _ in range(4)]
+    for t in range(cfg.max_ctx - 1):
+        pos = torch.full((B,), t, dtype=torch.int32, device=dev)
+        k, v = pool[t % 4]
+        for l in range(cfg.n_layers):
+            model.kv.kv_update(l, k, v, pos)
+    tokens = torch.randint(0, cfg.vocab, (B,), generator=g, device=dev, dtype=torch.int32)
+    pos = torch.full((B,), cfg.max_ctx - 1, dtype=torch.int32, device=dev)
+    for _ in range(max(1, args.warmup)):
+        model.step(tokens, pos)
+    torch.cuda.synchronize()
+    steps = max(3, args.steps // 5)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        model.step(tokens, pos)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    nxt = model.next.cpu()
+    return {"workload": "c4 decode step: 20B shape, 24 layers, vocabulary 201088, 512 sequences at "
+                        "position 1023 (window 128 on even layers, 128 bf16 tokens on odd layers)",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1), "steps": steps,
+            "next_tokens_in_range": bool(((nxt >= 0) & (nxt < cfg.vocab)).all()),
+            "note": "each timed step rewrites position 1023's cache rows and attends over 1024 "
+                    "positions; dense projections on torch.matmul (hipBLASLt)"}
+
+
 def time_variants(layers, x, out, fi, fw, args, c, flops):
     """Extra measured variants (never the headline): the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
@@ -403,6 +448,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.attn_only:
         print(json.dumps({"c4_attention": time_c4_attention(args, dev)}))
+        return
+    if args.decoder_only:
+        print(json.dumps({"c4_decoder": time_c4_decoder(args, dev)}))
         return
     d = synth.make_data(args.config)
     c = d.cfg
@@ -517,6 +565,11 @@ def main():
             res["c4_attention"] = time_c4_attention(args, dev)
         except Exception as e:  # an extra line: report, never fail the headline
             res["c4_attention"] = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.empty_cache()
+        try:
+            res["c4_decoder"] = time_c4_decoder(args, dev)
+        except Exception as e:  # an extra line: report, never fail the headline
+            res["c4_decoder"] = {"error": f"{type(e).__name__}: {e}"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
     else:

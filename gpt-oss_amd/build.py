@@ -19,7 +19,7 @@ HIP_FLAGS = [
 
 SOURCES = [os.path.join(HERE, "csrc", "gptoss_moe.hip"), os.path.join(HERE, "csrc", "bin_loader.cpp")]
 LIB = os.path.join(HERE, "libgptoss_moe.so")
-ATTN_SOURCES = [os.path.join(HERE, "csrc", "gptoss_attn.hip")]
+ATTN_SOURCES = [os.path.join(HERE, "csrc", "gptoss_attn.hip"), os.path.join(HERE, "csrc", "gptoss_decoder.hip")]
 ATTN_LIB = os.path.join(HERE, "libgptoss_attn.so")
 
 

@@ -38,6 +38,12 @@
 
 #include "gptoss_attn.h"
 
+// The last failed HIP call of this thread, for every entry point of the
+// library (gptoss_decoder.hip records its own here too).
+namespace gptoss_attn_detail {
+thread_local int last_hip_error = 0;
+}
+
 namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -58,10 +64,8 @@ constexpr int kMaxSplits = 64;
 constexpr int kTargetWaves = 2048;  // 256 CUs x 8 waves
 constexpr float kLog2e = 1.4426950408889634f;
 
-thread_local int g_last_hip_error = 0;
-
 int hip_fail(hipError_t e) {
-    g_last_hip_error = (int)e;
+    gptoss_attn_detail::last_hip_error = (int)e;
     return GPTOSS_ATTN_ERR_HIP;
 }
 
@@ -741,6 +745,6 @@ int gptoss_attn_decode(const gptoss_attn_shape *shape, const gptoss_attn_cache *
     return GPTOSS_ATTN_OK;
 }
 
-int gptoss_attn_last_hip_error(void) { return g_last_hip_error; }
+int gptoss_attn_last_hip_error(void) { return gptoss_attn_detail::last_hip_error; }
 
 }  // extern "C"

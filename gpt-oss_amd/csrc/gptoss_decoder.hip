@@ -1,0 +1,237 @@
+// gptoss_decoder.hip — the per-token glue of a gpt-oss decode step for gfx950
+// (declared in gptoss_decoder.h): RoPE tables (host), QKV bias + rotary split,
+// output-projection epilogue, embedding gather, greedy sampling.  Each
+// device kernel moves 16 bytes per lane per access.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "gptoss_attn.h"
+#include "gptoss_decoder.h"
+
+namespace gptoss_attn_detail {
+extern thread_local int last_hip_error;  // gptoss_attn.hip
+}
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
+constexpr int kNq = 64, kNkv = 8, kHd = 64, kHalf = kHd / 2;
+constexpr int kQkvWidth = (kNq + 2 * kNkv) * kHd;  // 5120
+
+__device__ inline float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ inline uint32_t f2bf(float f) {  // nearest even; NaN stays NaN
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ inline float lo16(uint32_t w) { return bf2f(w & 0xffffu); }
+__device__ inline float hi16(uint32_t w) { return bf2f(w >> 16); }
+__device__ inline uint32_t pack(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+__device__ inline float bround(float x) { return bf2f(f2bf(x)); }  // through bf16
+
+// One 8-element unit per thread: query units (head, 8 pairs) 0..255, key
+// units 256..287, value units (8 elements) 288..351.
+constexpr int kQUnits = kNq * (kHalf / 8), kKUnits = kNkv * (kHalf / 8), kVUnits = kNkv * kHd / 8;
+
+__global__ __launch_bounds__(128) void qkv_rope_kernel(const uint16_t *__restrict__ qkv,
+                                                       const uint16_t *__restrict__ bias,
+                                                       const float *__restrict__ cos_tab,
+                                                       const float *__restrict__ sin_tab, int n_pos,
+                                                       const int32_t *__restrict__ pos,
+                                                       uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+                                                       uint16_t *__restrict__ v) {
+    const int b = blockIdx.x;
+    const int p = pos[b];
+    const bool ok = p >= 0 && p < n_pos;
+    const uint16_t *row = qkv + (size_t)b * kQkvWidth;
+    for (int u = threadIdx.x; u < kQUnits + kKUnits + kVUnits; u += blockDim.x) {
+        if (u < kQUnits + kKUnits) {
+            const bool isq = u < kQUnits;
+            const int uu = isq ? u : u - kQUnits;
+            const int head = uu >> 2, i0 = (uu & 3) * 8;                  // pairs i0 .. i0 + 7
+            const int e0 = (isq ? 0 : kNq * kHd) + head * kHd + i0;       // first-half element
+            uint16_t *dst = isq ? q + ((size_t)b * kNq + head) * kHd : k + ((size_t)b * kNkv + head) * kHd;
+            u32x4 o0 = {0u, 0u, 0u, 0u}, o1 = o0;
+            if (ok) {
+                const u32x4 x0 = *(const u32x4 *)(row + e0), x1 = *(const u32x4 *)(row + e0 + kHalf);
+                const u32x4 b0 = *(const u32x4 *)(bias + e0), b1 = *(const u32x4 *)(bias + e0 + kHalf);
+                const float *cs = cos_tab + (size_t)p * kHalf + i0, *sn = sin_tab + (size_t)p * kHalf + i0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float y0[2], y1[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const float a = bround((t ? hi16(x0[j]) : lo16(x0[j])) + (t ? hi16(b0[j]) : lo16(b0[j])));
+                        const float c2 = bround((t ? hi16(x1[j]) : lo16(x1[j])) + (t ? hi16(b1[j]) : lo16(b1[j])));
+                        const float c = cs[2 * j + t], s = sn[2 * j + t];
+                        y0[t] = fmaf(a, c, -(c2 * s));
+                        y1[t] = fmaf(c2, c, a * s);
+                    }
+                    o0[j] = pack(y0[0], y0[1]);
+                    o1[j] = pack(y1[0], y1[1]);
+                }
+            }
+            *(u32x4 *)(dst + i0) = o0;
+            *(u32x4 *)(dst + i0 + kHalf) = o1;
+        } else {
+            const int e = (kNq + kNkv) * kHd + (u - kQUnits - kKUnits) * 8;
+            u32x4 o = {0u, 0u, 0u, 0u};
+            if (ok) {
+                const u32x4 x = *(const u32x4 *)(row + e), bb = *(const u32x4 *)(bias + e);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = pack(lo16(x[j]) + lo16(bb[j]), hi16(x[j]) + hi16(bb[j]));
+            }
+            *(u32x4 *)(v + (size_t)b * kNkv * kHd + (e - (kNq + kNkv) * kHd)) = o;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void bias_residual_kernel(uint16_t *__restrict__ x,
+                                                            const uint16_t *__restrict__ proj,
+                                                            const uint16_t *__restrict__ bias,
+                                                            size_t n8, int hidden8) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
+        const u32x4 p = ((const u32x4 *)proj)[i], bb = ((const u32x4 *)bias)[i % hidden8];
+        u32x4 xv = ((u32x4 *)x)[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xv[j] = pack(bround(lo16(p[j]) + lo16(bb[j])) + lo16(xv[j]),
+                         bround(hi16(p[j]) + hi16(bb[j])) + hi16(xv[j]));
+        ((u32x4 *)x)[i] = xv;
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t *__restrict__ table, int vocab,
+                                                    int hidden8, const int32_t *__restrict__ tokens,
+                                                    uint16_t *__restrict__ x) {
+    const int b = blockIdx.x;
+    const int t = tokens[b];
+    const bool ok = t >= 0 && t < vocab;
+    for (int i = threadIdx.x; i < hidden8; i += blockDim.x)
+        ((u32x4 *)x)[(size_t)b * hidden8 + i] =
+            ok ? ((const u32x4 *)table)[(size_t)t * hidden8 + i] : u32x4{0u, 0u, 0u, 0u};
+}
+
+// Greedy sampling: strided scan, then (value, index) reductions in which the
+// larger value wins and, on equal values, the smaller index.
+__device__ inline void better(float &p, int &i, float p2, int i2) {
+    if (p2 > p || (p2 == p && i2 < i)) {
+        p = p2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t *__restrict__ logits, int n_cols,
+                                                     int32_t *__restrict__ out) {
+    __shared__ float sp[4];
+    __shared__ int si[4];
+    const int r = blockIdx.x;
+    const uint16_t *row = logits + (size_t)r * n_cols;
+    float bp = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < n_cols; i += blockDim.x) better(bp, bi, bf2f(row[i]), i);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) better(bp, bi, __shfl_xor(bp, o), __shfl_xor(bi, o));
+    if ((threadIdx.x & 63) == 0) {
+        sp[threadIdx.x >> 6] = bp;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) better(bp, bi, sp[w], si[w]);
+        out[r] = bi;  // a row of NaNs: INT32_MAX, as the reference
+    }
+}
+
+int launched() {
+    const hipError_t e = hipGetLastError();
+    if (e == hipSuccess) return GPTOSS_ATTN_OK;
+    gptoss_attn_detail::last_hip_error = (int)e;
+    return GPTOSS_ATTN_ERR_HIP;
+}
+
+bool aligned(const void *p, size_t n) { return p && ((uintptr_t)p % n) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int gptoss_dec_rope_table(float base, int head_dim, float scaling_factor, float initial_context_length,
+                          int n_pos, float *cos_out, float *sin_out) {
+#pragma clang fp contract(off)  // run.cpp's expressions, each operation rounded on its own
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 1024 || n_pos < 0 || !cos_out || !sin_out)
+        return GPTOSS_ATTN_ERR_INVALID_ARG;
+    const int d_half = head_dim / 2;
+    float inv_freq[512];
+    float concentration = 1.0f;
+    if (scaling_factor > 1.0f) {
+        concentration = 0.1f * logf(scaling_factor) + 1.0f;
+        const double pi = 3.14159265358979323846;  // run.cpp's M_PI: the quotient is a double
+        const float low = d_half * logf((float)(initial_context_length / (32.0f * 2.0f * pi))) / logf(base);
+        const float high = d_half * logf((float)(initial_context_length / (1.0f * 2.0f * pi))) / logf(base);
+        if (!(0 < low && low < high && high < d_half - 1)) return GPTOSS_ATTN_ERR_INVALID_ARG;
+        for (int i = 0; i < d_half; i++) {
+            const float freq = powf(base, ((float)(2 * i)) / (float)head_dim);
+            const float interpolation = 1.0f / (scaling_factor * freq);
+            const float extrapolation = 1.0f / freq;
+            float ramp = ((float)i - low) / (high - low);
+            ramp = ramp < 0 ? 0 : (ramp > 1 ? 1 : ramp);
+            const float mask = 1.0f - ramp;
+            inv_freq[i] = interpolation * (1.0f - mask) + extrapolation * mask;
+        }
+    } else {
+        for (int i = 0; i < d_half; i++) inv_freq[i] = 1.0f / powf(base, ((float)(2 * i)) / (float)head_dim);
+    }
+    for (int p = 0; p < n_pos; ++p)
+        for (int j = 0; j < d_half; j++) {
+            const float val = (float)p * inv_freq[j];
+            cos_out[(size_t)p * d_half + j] = cosf(val) * concentration;
+            sin_out[(size_t)p * d_half + j] = sinf(val) * concentration;
+        }
+    return GPTOSS_ATTN_OK;
+}
+
+int gptoss_dec_qkv_rope(const uint16_t *qkv, const uint16_t *bias, const float *cos_tab,
+                        const float *sin_tab, int n_pos, const int32_t *pos, int n_seqs, uint16_t *q,
+                        uint16_t *k, uint16_t *v, hipStream_t stream) {
+    if (n_seqs < 0 || n_pos < 0) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    if (n_seqs == 0) return GPTOSS_ATTN_OK;
+    if (!aligned(qkv, 16) || !aligned(bias, 16) || !aligned(cos_tab, 4) || !aligned(sin_tab, 4) ||
+        !aligned(pos, 4) || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+        return GPTOSS_ATTN_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(qkv_rope_kernel, dim3(n_seqs), dim3(128), 0, stream, qkv, bias, cos_tab, sin_tab,
+                       n_pos, pos, q, k, v);
+    return launched();
+}
+
+int gptoss_dec_bias_residual(uint16_t *x, const uint16_t *proj, const uint16_t *bias, int n_rows,
+                             int hidden, hipStream_t stream) {
+    if (n_rows < 0 || hidden <= 0 || hidden % 8) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    if (n_rows == 0) return GPTOSS_ATTN_OK;
+    if (!aligned(x, 16) || !aligned(proj, 16) || !aligned(bias, 16)) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    const size_t n8 = (size_t)n_rows * hidden / 8;
+    const int blocks = (int)((n8 + 255) / 256 < 4096 ? (n8 + 255) / 256 : 4096);
+    hipLaunchKernelGGL(bias_residual_kernel, dim3(blocks), dim3(256), 0, stream, x, proj, bias, n8, hidden / 8);
+    return launched();
+}
+
+int gptoss_dec_embed(const uint16_t *table, int vocab, int hidden, const int32_t *tokens, int n,
+                     uint16_t *x, hipStream_t stream) {
+    if (n < 0 || vocab <= 0 || hidden <= 0 || hidden % 8) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    if (n == 0) return GPTOSS_ATTN_OK;
+    if (!aligned(table, 16) || !aligned(tokens, 4) || !aligned(x, 16)) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream, table, vocab, hidden / 8, tokens, x);
+    return launched();
+}
+
+int gptoss_dec_argmax(const uint16_t *logits, int n_rows, int n_cols, int32_t *out, hipStream_t stream) {
+    if (n_rows < 0 || n_cols <= 0) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    if (n_rows == 0) return GPTOSS_ATTN_OK;
+    if (!aligned(logits, 2) || !aligned(out, 4)) return GPTOSS_ATTN_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(argmax_kernel, dim3(n_rows), dim3(256), 0, stream, logits, n_cols, out);
+    return launched();
+}
+
+}  // extern "C"

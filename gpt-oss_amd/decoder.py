@@ -1,0 +1,216 @@
+"""A gpt-oss decode step on one MI355X (config C4 of the benchmark): the
+reference's forward_batch_gpu (getp-csrc/getp_run.cpp:3260-3409) for one
+token per sequence, over the libraries of this package:
+
+    x = embed(tokens)                                  gptoss_dec_embed
+    per layer l:
+        t = RMSNorm(x)                                 gptoss_moe_rmsnorm
+        qkv = t Wqkv^T                                 library GEMM (bf16 out)
+        q, k, v = RoPE(qkv + b_qkv)                    gptoss_dec_qkv_rope
+        KV-cache update; o = attention(q)              gptoss_attn_kv_update / _decode
+        x = x + (o Wo^T + b_o)                         library GEMM + gptoss_dec_bias_residual
+        x = x + MoE(RMSNorm(x))                        gptoss_moe_layer
+    logits = RMSNorm(x) Wout^T; next = argmax           library GEMM + gptoss_dec_argmax
+
+The dense projections are plain bf16 GEMMs and go to the platform library
+(torch.matmul -> hipBLASLt, fp32 accumulation, bf16 output, the reference's
+rounding point); everything else runs in this package's HIP kernels.  There
+is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+from typing import Optional
+
+import numpy as np
+
+import gptoss_attn as ga
+import gptoss_moe as gm
+
+N_HEADS, N_KV, HD = ga.N_HEADS, ga.N_KV_HEADS, ga.HEAD_DIM
+QKV_WIDTH = (N_HEADS + 2 * N_KV) * HD  # 5120
+
+
+@dataclasses.dataclass(frozen=True)
+class DecoderConfig:
+    """Config fields of run.cpp:25-45 that the decode step uses."""
+    hidden: int = 2880
+    intermediate: int = 2880
+    n_experts: int = 32
+    top_k: int = 4
+    n_layers: int = 24
+    vocab: int = 201088
+    max_ctx: int = 1024
+    sliding_window: int = 128
+    keep: int = 128
+    prefix_rule: int = ga.PREFIX_MIXED
+    rope_theta: float = 150000.0
+    rope_scaling: float = 32.0
+    initial_context_length: float = 4096.0
+
+
+def rope_table(cfg: DecoderConfig):
+    """Host cos/sin tables [max_ctx][32] (gptoss_dec_rope_table)."""
+    lib = ga.load_library()
+    c = np.empty((cfg.max_ctx, HD // 2), np.float32)
+    s = np.empty_like(c)
+    rc = lib.gptoss_dec_rope_table(cfg.rope_theta, HD, cfg.rope_scaling, cfg.initial_context_length,
+                                   cfg.max_ctx, c.ctypes.data, s.ctypes.data)
+    ga._check("gptoss_dec_rope_table", rc)
+    return c, s
+
+
+def _bf16(t):
+    import torch
+    return t if t.dtype == torch.bfloat16 else t.view(torch.bfloat16)
+
+
+class Decoder:
+    """Device weights, KV caches and scratch for `n_seqs` sequences.
+
+    weights: dict of device tensors (bf16 as torch.bfloat16 or int16 bits):
+      emb [vocab][H], out [vocab][H], rms_out [H], and per layer lists
+      rms_attn [H], w_qkv [5120][H], b_qkv [5120], w_o [H][4096], b_o [H],
+      sinks [64], rms_ffn [H]; moe: list of gptoss_moe.MoeLayer."""
+
+    def __init__(self, cfg: DecoderConfig, n_seqs: int, weights: dict, moe: list, device="cuda"):
+        import torch
+        self.cfg, self.n_seqs, self.dev = cfg, n_seqs, torch.device(device)
+        self.w = weights
+        self.moe = moe
+        self.lib = ga.load_library()
+        self.kv = ga.KvCache(n_seqs, cfg.n_layers, cfg.max_ctx, sliding_window=cfg.sliding_window,
+                             keep=cfg.keep, prefix_rule=cfg.prefix_rule, device=device)
+        c, s = rope_table(cfg)
+        self.cos = torch.from_numpy(c).to(self.dev)
+        self.sin = torch.from_numpy(s).to(self.dev)
+        B, H = n_seqs, cfg.hidden
+        bf = torch.bfloat16
+        self.x = torch.empty((B, H), dtype=bf, device=self.dev)
+        self.t = torch.empty((B, H), dtype=bf, device=self.dev)
+        self.qkv = torch.empty((B, QKV_WIDTH), dtype=bf, device=self.dev)
+        self.q = torch.empty((B, N_HEADS, HD), dtype=bf, device=self.dev)
+        self.k = torch.empty((B, N_KV * HD), dtype=bf, device=self.dev)
+        self.v = torch.empty((B, N_KV * HD), dtype=bf, device=self.dev)
+        self.o = torch.empty((B, N_HEADS, HD), dtype=bf, device=self.dev)
+        self.proj = torch.empty((B, H), dtype=bf, device=self.dev)
+        self.logits = torch.empty((B, cfg.vocab), dtype=bf, device=self.dev)
+        self.next = torch.empty((B,), dtype=torch.int32, device=self.dev)
+
+    def _st(self):
+        return ga._stream(None)
+
+    def step(self, tokens, pos, trace: Optional[list] = None):
+        """One decode step: tokens, pos int32 [n_seqs] (device).  Returns the
+        next tokens (device int32 [n_seqs]); self.logits holds the logits.
+        trace: if a list, per layer a dict of CPU copies of the
+        intermediates is appended (tests)."""
+        import torch
+        cfg, lib, B, H = self.cfg, self.lib, self.n_seqs, self.cfg.hidden
+        st = self._st()
+        w = self.w
+        ga._check("gptoss_dec_embed", lib.gptoss_dec_embed(w["emb"].data_ptr(), cfg.vocab, H,
+                                                          tokens.data_ptr(), B, self.x.data_ptr(), st))
+        for l in range(cfg.n_layers):
+            rec = {"x_in": self.x.clone()} if trace is not None else None
+            gm.rmsnorm(self.x.view(torch.int16), w["rms_attn"][l], out=self.t.view(torch.int16))
+            torch.matmul(self.t, _bf16(w["w_qkv"][l]).t(), out=self.qkv)
+            ga._check("gptoss_dec_qkv_rope",
+                      lib.gptoss_dec_qkv_rope(self.qkv.data_ptr(), w["b_qkv"][l].data_ptr(),
+                                              self.cos.data_ptr(), self.sin.data_ptr(), cfg.max_ctx,
+                                              pos.data_ptr(), B, self.q.data_ptr(), self.k.data_ptr(),
+                                              self.v.data_ptr(), st))
+            self.kv.kv_update(l, self.k, self.v, pos)
+            self.kv.decode(l, self.q, w["sinks"][l], pos, out=self.o)
+            if rec is not None:
+                rec.update(t=self.t.clone(), qkv=self.qkv.clone(), q=self.q.clone(), k=self.k.clone(),
+                           v=self.v.clone(), o=self.o.clone())
+            torch.matmul(self.o.view(B, N_HEADS * HD), _bf16(w["w_o"][l]).t(), out=self.proj)
+            ga._check("gptoss_dec_bias_residual",
+                      lib.gptoss_dec_bias_residual(self.x.data_ptr(), self.proj.data_ptr(),
+                                                   w["b_o"][l].data_ptr(), B, H, st))
+            if rec is not None:
+                rec.update(proj=self.proj.clone(), x_attn=self.x.clone())
+            self.moe[l].layer(self.x.view(torch.int16), w["rms_ffn"][l], t_scratch=self.t.view(torch.int16))
+            if rec is not None:
+                rec["x_out"] = self.x.clone()
+                trace.append({k: v.view(torch.int16).cpu().numpy().view(np.uint16) for k, v in rec.items()})
+        gm.rmsnorm(self.x.view(torch.int16), w["rms_out"], out=self.t.view(torch.int16))
+        torch.matmul(self.t, _bf16(w["out"]).t(), out=self.logits)
+        ga._check("gptoss_dec_argmax", lib.gptoss_dec_argmax(self.logits.data_ptr(), B, cfg.vocab,
+                                                            self.next.data_ptr(), st))
+        return self.next
+
+
+def make_host_weights(cfg: DecoderConfig, seed: int = 0xDEC0DE):
+    """Random-init weights of the architecture as numpy (bf16 bits; MoE
+    layers as synth.MoeData), for tests at small shapes."""
+    import synth
+    rng = np.random.Generator(np.random.PCG64(seed))
+    H, L = cfg.hidden, cfg.n_layers
+    nb = lambda shape, sigma: synth.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma))
+    ones = lambda: synth.f32_to_bf16((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    w = {"emb": nb((cfg.vocab, H), 1.0), "out": nb((cfg.vocab, H), H ** -0.5), "rms_out": ones(),
+         "rms_attn": [], "w_qkv": [], "b_qkv": [], "w_o": [], "b_o": [], "sinks": [], "rms_ffn": []}
+    moe = []
+    for l in range(L):
+        w["rms_attn"].append(ones())
+        w["w_qkv"].append(nb((QKV_WIDTH, H), H ** -0.5))
+        w["b_qkv"].append(nb(QKV_WIDTH, 0.1))
+        w["w_o"].append(nb((H, N_HEADS * HD), (N_HEADS * HD) ** -0.5))
+        w["b_o"].append(nb(H, 0.01))
+        w["sinks"].append(nb(N_HEADS, 1.0))
+        w["rms_ffn"].append(ones())
+        mc = synth.MoeConfig(f"dec_l{l}", H, cfg.intermediate, cfg.n_experts, cfg.top_k, 1, "router",
+                             seed + 1 + l)
+        moe.append(synth.make_data(mc))
+    return w, moe
+
+
+def from_host(cfg: DecoderConfig, n_seqs: int, w: dict, moe_data: list, device="cuda") -> Decoder:
+    import torch
+    dev = torch.device(device)
+    up = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    dw = {k: ([up(a) for a in v] if isinstance(v, list) else up(v)) for k, v in w.items()}
+    moe = []
+    for d in moe_data:
+        lay = gm.MoeLayer.from_numpy(d, max_tokens=n_seqs, device=device)
+        lay.drop_unpacked()
+        moe.append(lay)
+    return Decoder(cfg, n_seqs, dw, moe, device)
+
+
+def random_on_device(cfg: DecoderConfig, n_seqs: int, seed: int = 0xC4, device="cuda") -> Decoder:
+    """Random-init weights generated on the device (the full 20B shape does
+    not fit a host round trip quickly): MoE weights packed, originals freed."""
+    import torch
+    dev = torch.device(device)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    H, L = cfg.hidden, cfg.n_layers
+    nb = lambda shape, sigma: (torch.randn(shape, generator=g, device=dev) * sigma).to(torch.bfloat16)
+    ones = lambda: (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    w = {"emb": nb((cfg.vocab, H), 1.0), "out": nb((cfg.vocab, H), H ** -0.5), "rms_out": ones(),
+         "rms_attn": [ones() for _ in range(L)], "w_qkv": [nb((QKV_WIDTH, H), H ** -0.5) for _ in range(L)],
+         "b_qkv": [nb(QKV_WIDTH, 0.1) for _ in range(L)],
+         "w_o": [nb((H, N_HEADS * HD), (N_HEADS * HD) ** -0.5) for _ in range(L)],
+         "b_o": [nb(H, 0.01) for _ in range(L)], "sinks": [nb(N_HEADS, 1.0) for _ in range(L)],
+         "rms_ffn": [ones() for _ in range(L)]}
+    w = {k: ([t.view(torch.int16) for t in v] if isinstance(v, list) else v.view(torch.int16))
+         for k, v in w.items()}
+    E, D = cfg.n_experts, cfg.intermediate
+    n1, n2 = E * 2 * D * H, E * H * D
+    u8 = lambda n, lo, hi: torch.randint(lo, hi, (n,), generator=g, device=dev, dtype=torch.uint8)
+    shape = gm.make_shape(H, D, E, cfg.top_k)
+    moe = []
+    for _ in range(L):
+        mw = {"router_w": nb((E, H), 0.02).view(torch.int16), "router_b": nb((E,), 0.01).view(torch.int16),
+              "w1": u8(n1 // 2, 0, 256), "w1_scales": u8(n1 // 32, 120, 129),
+              "b1": nb((E, 2 * D), 0.01).view(torch.int16),
+              "w2": u8(n2 // 2, 0, 256), "w2_scales": u8(n2 // 32, 120, 129),
+              "b2": nb((E, H), 0.01).view(torch.int16)}
+        lay = gm.MoeLayer(shape, mw, n_seqs, device)
+        lay.drop_unpacked()
+        moe.append(lay)
+    return Decoder(cfg, n_seqs, w, moe, device)

@@ -58,6 +58,13 @@ _SIGS = {
     "gptoss_attn_decode": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P,
                                           ctypes.c_size_t, _P]),
     "gptoss_attn_last_hip_error": (ctypes.c_int, []),
+    # the decode-step glue of include/gptoss_decoder.h (same library)
+    "gptoss_dec_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                             ctypes.c_int, _P, _P]),
+    "gptoss_dec_qkv_rope": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int, _P, _P, _P, _P]),
+    "gptoss_dec_bias_residual": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, ctypes.c_int, _P]),
+    "gptoss_dec_embed": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int, _P, _P]),
+    "gptoss_dec_argmax": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _P, _P]),
 }
 
 _lib = None

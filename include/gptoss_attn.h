@@ -138,7 +138,8 @@ int gptoss_attn_decode(const gptoss_attn_shape *shape, const gptoss_attn_cache *
                        const int32_t *pos, int n_seqs, uint16_t *out, void *ws, size_t ws_bytes,
                        hipStream_t stream);
 
-/* hipError_t of the last failed HIP call in this thread (0 if none). */
+/* hipError_t of the last failed HIP call in this thread (0 if none), for
+ * the entry points of gptoss_attn.h and gptoss_decoder.h. */
 int gptoss_attn_last_hip_error(void);
 
 #ifdef __cplusplus

@@ -1,0 +1,71 @@
+/*
+ * gptoss_decoder.h — C ABI of the per-token glue of a gpt-oss decode step on
+ * MI355X (gfx950), around the attention of gptoss_attn.h and the MoE layer of
+ * gptoss_moe.h: the RoPE tables, the QKV bias + rotary split, the
+ * output-projection epilogue, the embedding gather and greedy sampling.
+ * The dense projections themselves (QKV, output, unembedding) are plain bf16
+ * GEMMs left to a library GEMM (hipBLASLt).
+ *
+ * Every device entry point takes plain pointers, sizes and a HIP stream and
+ * returns an int status (0 = ok, negative = GPTOSS_ATTN_ERR_*); none
+ * allocates, exits or synchronises the host.  bf16 values are uint16_t bit
+ * patterns.
+ */
+#ifndef GPTOSS_DECODER_H
+#define GPTOSS_DECODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Host function (no device work): RoPE cos/sin tables with YaRN scaling,
+ * cos_out/sin_out [n_pos][head_dim / 2] fp32 in host memory, as
+ * compute_concentration_and_inv_freq + compute_cos_sin (run.cpp:422-503),
+ * which the reference evaluates on the host to fill its device tables
+ * (getp_run.cpp:1876-1890); ntk_beta 32, ntk_alpha 1 (run.cpp:576-577).
+ * Returns GPTOSS_ATTN_ERR_INVALID_ARG where run.cpp's assertion on the YaRN
+ * band edges would fail. */
+int gptoss_dec_rope_table(float rope_theta, int head_dim, float rope_scaling_factor,
+                          float initial_context_length, int n_pos, float *cos_out, float *sin_out);
+
+/* QKV bias + split + rotary (add_bias_kernel, other_kernels.hpp:53-61, and
+ * launch_split_qkv_apply_rotary_bf16, rope.hpp:346-380, launched at
+ * getp_run.cpp:2290-2310): qkv bf16 [n_seqs][(64 + 2*8) * 64] is the QKV
+ * GEMM output; each element becomes bf16(x + bias); query and key head pairs
+ * (i, i + 32) at position pos[b] become bf16(a c - b s), bf16(b c + a s)
+ * with c, s from the device tables cos/sin [n_pos][32] (fp32, evaluated as
+ * fmaf(a, c, -(b s)) and fmaf(b, c, a s)); values are copied.  Outputs: q
+ * [n_seqs][64][64], k and v [n_seqs][512].  A sequence with pos outside
+ * [0, n_pos) gets zeros. */
+int gptoss_dec_qkv_rope(const uint16_t *qkv, const uint16_t *bias, const float *cos_tab,
+                        const float *sin_tab, int n_pos, const int32_t *pos, int n_seqs,
+                        uint16_t *q, uint16_t *k, uint16_t *v, hipStream_t stream);
+
+/* Output-projection epilogue (store_and_fuse_tile_bf16, matmul.hpp:121-139,
+ * of the fused output projection at getp_run.cpp:2465-2481):
+ * x[r][h] = bf16(bf16(proj[r][h] + bias[h]) + x[r][h]), proj the GEMM output
+ * in bf16.  hidden a multiple of 8. */
+int gptoss_dec_bias_residual(uint16_t *x, const uint16_t *proj, const uint16_t *bias, int n_rows,
+                             int hidden, hipStream_t stream);
+
+/* Embedding gather (copy_embeddings_kernel_bf16, other_kernels.hpp:114-135):
+ * x[b] = table[tokens[b]] (bf16 rows of `hidden`, a multiple of 8); a token
+ * outside [0, vocab) gives a zero row. */
+int gptoss_dec_embed(const uint16_t *table, int vocab, int hidden, const int32_t *tokens, int n,
+                     uint16_t *x, hipStream_t stream);
+
+/* Greedy sampling (sample_argmax_bf16, softmax.hpp:236-300): out[r] = the
+ * first index of the largest value of bf16 row r of logits [n_rows][n_cols]
+ * (NaN never wins; a row of NaNs gives INT32_MAX, as in the reference). */
+int gptoss_dec_argmax(const uint16_t *logits, int n_rows, int n_cols, int32_t *out,
+                      hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPTOSS_DECODER_H */

@@ -105,3 +105,48 @@ def test_bad_buffers_rejected():
                                   p, None, 0, None) == ga.ERR_INVALID_ARG
     # zero sequences: nothing to do
     assert call_both(s, c, L, n=0) == (ga.OK, ga.OK)
+
+
+# ---- the decode-step glue (include/gptoss_decoder.h, same library) ----
+DEC_HEADER = os.path.join(ROOT, "include", "gptoss_decoder.h")
+
+
+def test_decoder_glue_exports():
+    lib = ga.load_library()
+    text = re.sub(r"/\*.*?\*/", "", open(DEC_HEADER).read(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(gptoss_dec_\w+)\s*\(", text)))
+    assert len(names) == 5
+    assert not [n for n in names if not hasattr(lib, n)]
+    assert set(names) <= set(ga._SIGS)
+
+
+def test_rope_table_host_function_matches_oracle_bit_for_bit():
+    import numpy as np
+    import oracle
+    import decoder
+    cfg = decoder.DecoderConfig(max_ctx=1024)
+    c, s = decoder.rope_table(cfg)
+    oc, os_ = oracle.rope_table(1024)
+    assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+    # an unscaled table, and run.cpp's assertion on the YaRN bands
+    lib = ga.load_library()
+    c1 = np.empty((8, 32), np.float32)
+    s1 = np.empty_like(c1)
+    assert lib.gptoss_dec_rope_table(10000.0, 64, 1.0, 4096.0, 8, c1.ctypes.data, s1.ctypes.data) == 0
+    assert np.allclose(c1[1], np.cos(10000.0 ** (-np.arange(32) / 32.0)), atol=1e-6)
+    assert lib.gptoss_dec_rope_table(150000.0, 64, 32.0, 64.0, 8, c1.ctypes.data,
+                                     s1.ctypes.data) == ga.ERR_INVALID_ARG
+
+
+def test_decoder_glue_rejects():
+    lib = ga.load_library()
+    p = 1 << 20
+    assert lib.gptoss_dec_qkv_rope(p + 2, p, p, p, 16, p, 4, p, p, p, None) == ga.ERR_INVALID_ARG
+    assert lib.gptoss_dec_qkv_rope(p, p, p, p, 16, p, -1, p, p, p, None) == ga.ERR_INVALID_ARG
+    assert lib.gptoss_dec_bias_residual(p, p, p, 4, 100, None) == ga.ERR_INVALID_ARG
+    assert lib.gptoss_dec_embed(p, 0, 64, p, 4, p, None) == ga.ERR_INVALID_ARG
+    assert lib.gptoss_dec_argmax(p, 4, 0, p, None) == ga.ERR_INVALID_ARG
+    # nothing to do
+    assert lib.gptoss_dec_qkv_rope(None, None, None, None, 16, None, 0, None, None, None, None) == ga.OK
+    assert lib.gptoss_dec_argmax(None, 0, 10, None, None) == ga.OK
