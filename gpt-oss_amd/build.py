@@ -27,6 +27,10 @@ ATTN_LIB = os.path.join(HERE, "libgptoss_attn.so")
 # run by tests/test_gpu_cpp_shim.py; links the in-tree library by rpath.
 SHIM_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "moe_gpu_test.cpp")
 SHIM_TEST_BIN = os.path.join(HERE, "bin", "moe_gpu_test")
+# The same for the attention shim (csrc/attn_gpu_shim.hpp), run by
+# tests/test_zzz_gpu_attn.py.
+ATTN_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "attn_gpu_test.cpp")
+ATTN_TEST_BIN = os.path.join(HERE, "bin", "attn_gpu_test")
 
 
 def _run(cmd, verbose):
@@ -48,6 +52,11 @@ def build(verbose: bool = False) -> str:
           "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
           "-x", "hip", SHIM_TEST_SRC, "-L", HERE, "-lgptoss_moe",
           "-Wl,-rpath,$ORIGIN/..", "-o", SHIM_TEST_BIN], verbose)
+    _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
+          "-x", "hip", ATTN_TEST_SRC, "-L", HERE, "-lgptoss_attn",
+          "-Wl,-rpath,$ORIGIN/..", "-o", ATTN_TEST_BIN], verbose)
     return LIB
 
 

@@ -146,3 +146,45 @@ def test_small_batch_split_matches_unsplit():
     assert np.max(np.abs(a - b)) <= 2 ** -7 * max(1.0, np.abs(a).max())
     want = f32_to_bf16(oracle_out(c, prefix_rule=0))
     parity.assert_close(f32_to_bf16(b), want, "attn split 1024")
+
+
+def test_cpp_attention_shim(tmp_path):
+    """The attention shim from C++ (tests/cpp/attn_gpu_test.cpp over
+    gpt-oss_amd/csrc/attn_gpu_shim.hpp, the reference's state member names):
+    40 steps of 2 layers (a 32-row ring, 16 bf16-kept tokens, the mixed
+    rule), the last step's outputs against the oracle, and the same step run
+    as two row ranges (row_offset) bit-identical to the whole batch."""
+    import os
+    import subprocess
+    from attn_cases import AttnCase, write_caches
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = os.path.join(root, "gpt-oss_amd", "bin", "attn_gpu_test")
+    assert os.path.exists(exe), "build it with __graft_entry__.build()"
+    B, L, max_seq, window, keep, rule, T = 4, 2, 64, 32, 16, 1, 40
+    rng = np.random.default_rng(21)
+    mag = np.exp(rng.normal(0, 0.5, size=(T, B, 1))).astype(np.float32)
+    kh = f32_to_bf16(rng.standard_normal((T, B, KV)).astype(np.float32) * mag)
+    vh = f32_to_bf16(rng.standard_normal((T, B, KV)).astype(np.float32) * mag)
+    q = f32_to_bf16(rng.standard_normal((B, 64, 64)).astype(np.float32))
+    sinks = f32_to_bf16(rng.standard_normal((L, 64)).astype(np.float32))
+    inp = tmp_path / "in.bin"
+    with open(inp, "wb") as f:
+        f.write(np.array([B, L, max_seq, window, keep, rule, T], np.int32).tobytes())
+        for t in range(T):
+            f.write(kh[t].tobytes())
+            f.write(vh[t].tobytes())
+        f.write(q.tobytes())
+        f.write(sinks.tobytes())
+    outp = tmp_path / "out.bin"
+    r = subprocess.run([exe, str(inp), str(outp)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0
+    out = np.fromfile(outp, np.uint16).reshape(2, L, B, 64, 64)
+    assert np.array_equal(out[0], out[1]), "row ranges differ from the whole batch"
+    for l in range(L):
+        c = AttnCase(l, window, keep, window if l % 2 == 0 else max_seq, np.full(B, T - 1, np.int32), q,
+                     [kh[:, b] for b in range(B)], [vh[:, b] for b in range(B)], sinks[l])
+        write_caches(c)
+        want = f32_to_bf16(oracle_out(c, prefix_rule=rule))
+        m = parity.assert_close(out[0, l], want, f"attention shim from C++, layer {l}")
+        assert m["rel_l2"] <= TIGHT_REL_L2, m
