@@ -538,9 +538,11 @@ __device__ __forceinline__ int n_mod8(int n, int x) { return n > x ? (n - 1 - x)
 // deal.  That balances tiles per XCD within 2, and both tiles of a unit share
 // one XCD's L2 (the GEMM streams the unit's weights once for both).  Tiles of
 // XCD x occupy tiles[xstart(x) .. xstart(x) + xcount(x)), 2-tile units first.
+// Experts with big_rows rows or more get no tiles here (the large-M GEMM on
+// packed weights takes them); their rows still count in counts and offsets.
 __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ counts,
                             int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *hdr,
-                            int E, int tr, int lane, bool write) {
+                            int E, int tr, int big_rows, int lane, bool write) {
     // lane l owns experts 4l .. 4l+3
     int c[4], nt[4], n2[4], n1[4];
     int csum = 0, s2 = 0, s1 = 0;
@@ -548,7 +550,7 @@ __device__ void build_tiles(const int *tot, int *offs, int32_t *__restrict__ cou
     for (int j = 0; j < 4; ++j) {
         const int e = 4 * lane + j;
         c[j] = e < E ? tot[e] : 0;
-        nt[j] = (c[j] + tr - 1) / tr;
+        nt[j] = c[j] >= big_rows ? 0 : (c[j] + tr - 1) / tr;
         n2[j] = nt[j] / 2;
         n1[j] = nt[j] % 2;
         csum += c[j];
@@ -660,7 +662,7 @@ __host__ __device__ constexpr int index_arrivals(int G, int n_blk) { return G * 
 __global__ __launch_bounds__(256) void index_kernel(
     int32_t *__restrict__ hist, int n_blk, const int32_t *__restrict__ slot_e,
     const uint16_t *__restrict__ topk_w, const uint16_t *__restrict__ x, int T, int K, int E,
-    int H, int block_tokens, int tile_rows, int32_t *__restrict__ counts,
+    int H, int block_tokens, int tile_rows, int big_rows, int32_t *__restrict__ counts,
     int32_t *__restrict__ offsets, Tile *__restrict__ tiles, int32_t *__restrict__ hdr,
     int32_t *__restrict__ local_ids, int32_t *__restrict__ row_token, float *__restrict__ row_w,
     int32_t *__restrict__ row_slot, uint16_t *__restrict__ xg) {
@@ -724,7 +726,7 @@ __global__ __launch_bounds__(256) void index_kernel(
     }
     __syncthreads();
     if (planner) {
-        if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tile_rows, tid, true);
+        if (tid < 64) build_tiles(tot, offs, counts, offsets, tiles, hdr, E, tile_rows, big_rows, tid, true);
     } else {
         if (tid < 64) expert_offsets(tot, offs, E, tid);
         __syncthreads();
@@ -1342,11 +1344,30 @@ __device__ __forceinline__ int lrow_of(int r) {  // weight row (in block) -> LDS
     return kMlp1 ? ((r & 1) << 7) | (r >> 1) : r;
 }
 
-template <bool kMlp1>
+// The large-M GEMM on packed weights (the per-expert tile switch of the
+// streamed path): the stage's weight chunk of block nb is packed column
+// tiles 16 nb .. 16 nb + 15 (packed rows 256 nb .. 256 nb + 255 hold exactly
+// the block's rows for MLP1 and MLP2), loaded 16 B per thread from the
+// contiguous 1 KB lane blocks and scattered as 4 dwords into the LDS row
+// format above: lane entry (n, g) of tile t carries bytes 16 q + 4 g (q =
+// 0..3) of packed row 16 t + n, LDS row R = (t & 1) 128 + 16 (t >> 1) + n for
+// MLP1 (gate tiles even, up tiles odd), 16 t + n for MLP2.  Scales: the
+// packed word of (stage, tile, n) is that row's 4 e8m0 bytes of the stage
+// (zero past K / 32, as the nibbles).  MLP1 reads x through the row map
+// (a_token), as the streamed GEMM.  Only experts with at least min_rows rows
+// take part; the streamed GEMM's tile list leaves them out.
+struct LPacked {
+    const uint8_t *w;        // packed nibbles of this matrix (nullptr: the reference layout)
+    const uint8_t *s;        // packed scales [e][kp][ct][16 rows][4 B]
+    const int32_t *a_token;  // MLP1: compact row -> x row; nullptr: A is row-compact
+    int min_rows;            // experts with fewer rows are left out
+};
+
+template <bool kMlp1, bool kPacked>
 __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
                                                                    const int32_t *__restrict__ counts,
                                                                    const int32_t *__restrict__ offsets,
-                                                                   int E) {
+                                                                   int E, LPacked pk) {
     __shared__ LStage buf[2];
     __shared__ LTile tiles[kLMaxTiles];
     __shared__ int s_ntiles;
@@ -1361,7 +1382,8 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
         int n = 0;
         for (int e0 = xcd; e0 < E; e0 += 8 * 64) {
             const int e = e0 + 8 * lane;
-            const int c = e < E ? counts[e] : 0;
+            const int c0 = e < E ? counts[e] : 0;
+            const int c = c0 >= pk.min_rows ? c0 : 0;
             const int o = e < E ? offsets[e] : 0;
             const int nt = (c + kLBM - 1) / kLBM;
             const int inc = wave_scan(nt, lane);
@@ -1403,21 +1425,43 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int q = tid + 512 * i, row = q >> 4, u = q & 15;
-            const uint32_t off = (uint32_t)min(row, tl.rows - 1) * (2u * K) +
-                                 2u * (uint32_t)min(j * kLBK + 8 * u, K - 8);
-            ra[r][i] = *reinterpret_cast<const u32x4 *>(abase + off);
+            const uint32_t kof = 2u * (uint32_t)min(j * kLBK + 8 * u, K - 8);
+            if (pk.a_token != nullptr) {  // x row of compact row row0 + row
+                const int tok = pk.a_token[tl.row0 + min(row, tl.rows - 1)];
+                ra[r][i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(a.A) +
+                                                            (size_t)tok * (2u * K) + kof);
+            } else {
+                const uint32_t off = (uint32_t)min(row, tl.rows - 1) * (2u * K) + kof;
+                ra[r][i] = *reinterpret_cast<const u32x4 *>(abase + off);
+            }
         }
-        const uint8_t *wq = a.Wq + (size_t)tl.expert * ((size_t)N * K / 2);
+        if (kPacked) {
+            // 16 packed column tiles x 64 lane entries, one 16-byte entry per load
+            const int CT = N / 16;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
-            const uint32_t row = (uint32_t)min(nb * kLBN + r0, N - 1);
-            const uint32_t kb = (uint32_t)min(j * (kLBK / 2) + 16 * u, K / 2 - 16);
-            rb[r][i] = *reinterpret_cast<const u32x4 *>(wq + row * (uint32_t)(K / 2) + kb);
+            for (int i = 0; i < 2; ++i) {
+                const int q = tid + 512 * i, ct = min(nb * 16 + (q >> 6), CT - 1);
+                rb[r][i] = *reinterpret_cast<const u32x4 *>(
+                    pk.w + (((size_t)tl.expert * CT + ct) * NST + j) * 1024 + 16 * (q & 63));
+            }
+        } else {
+            const uint8_t *wq = a.Wq + (size_t)tl.expert * ((size_t)N * K / 2);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
+                const uint32_t row = (uint32_t)min(nb * kLBN + r0, N - 1);
+                const uint32_t kb = (uint32_t)min(j * (kLBK / 2) + 16 * u, K / 2 - 16);
+                rb[r][i] = *reinterpret_cast<const u32x4 *>(wq + row * (uint32_t)(K / 2) + kb);
+            }
         }
-        // waves 0..3: scales of block row tid; 4, 5: bias pair; 6, 7: token slot
+        // waves 0..3: scales of block row tid (packed: of tile tid / 16, row
+        // tid % 16); 4, 5: bias pair; 6, 7: token slot
         const uint16_t *p16;
-        if (wave < 4) {
+        if (wave < 4 && kPacked) {
+            const int CT = N / 16, ct = min(nb * 16 + (tid >> 4), CT - 1);
+            p16 = reinterpret_cast<const uint16_t *>(pk.s + (((size_t)tl.expert * NST + j) * CT + ct) * 64 +
+                                                     4 * (tid & 15));
+        } else if (wave < 4) {
             const uint32_t row = (uint32_t)min(nb * kLBN + tid, N - 1);
             p16 = reinterpret_cast<const uint16_t *>(a.Ws + (size_t)tl.expert * ((size_t)N * KS) +
                                                      row * (uint32_t)KS + min(4 * j, KS - 4));
@@ -1441,15 +1485,33 @@ __global__ __launch_bounds__(kLWaves * 64) void large_m_gemm_kernel(GemmArgs a,
             const int q = tid + 512 * i, row = q >> 4, u = q & 15;
             sb.a[row * 16 + (u ^ (row & 15))] = __builtin_bit_cast(uint4, ra[r][i]);
         }
+        if (kPacked) {
+            uint32_t *bw = reinterpret_cast<uint32_t *>(sb.b);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
-            const int R = lrow_of<kMlp1>(r0);
-            const uint32_t km = -(uint32_t)(nb * kLBN + r0 < N && j * kLBK + 32 * u < K);
-            const u32x4 v = rb[r][i];
-            sb.b[R * 4 + (u ^ ((R >> 2) & 3))] = make_uint4(v.x & km, v.y & km, v.z & km, v.w & km);
+            for (int i = 0; i < 2; ++i) {
+                const int q = tid + 512 * i, t = q >> 6, n = q & 15, gq = (q >> 4) & 3;
+                const int R = kMlp1 ? ((t & 1) << 7) + 16 * (t >> 1) + n : 16 * t + n;
+                const uint32_t km = -(uint32_t)(nb * 16 + t < N / 16);
+                const u32x4 v = rb[r][i];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) bw[(R * 4 + (u ^ ((R >> 2) & 3))) * 4 + gq] = v[u] & km;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int q = tid + 512 * i, r0 = q >> 2, u = q & 3;
+                const int R = lrow_of<kMlp1>(r0);
+                const uint32_t km = -(uint32_t)(nb * kLBN + r0 < N && j * kLBK + 32 * u < K);
+                const u32x4 v = rb[r][i];
+                sb.b[R * 4 + (u ^ ((R >> 2) & 3))] = make_uint4(v.x & km, v.y & km, v.z & km, v.w & km);
+            }
         }
-        if (wave < 4) {
+        if (wave < 4 && kPacked) {
+            const int t = tid >> 4, n = tid & 15;
+            const int R = kMlp1 ? ((t & 1) << 7) + 16 * (t >> 1) + n : 16 * t + n;
+            const uint32_t km = -(uint32_t)(nb * 16 + t < N / 16);
+            sb.s[R] = (rx[r][0] | (rx[r][1] << 16)) & km;
+        } else if (wave < 4) {
             // groups past K/32 (last stage) read as scale 0: weights there are zero
             uint32_t sv = rx[r][0] | (rx[r][1] << 16);
             const int ng = KS - 4 * j;  // valid groups of this stage (>= 2, K a multiple of 64)
@@ -2948,7 +3010,7 @@ bool shape_ok(const gptoss_moe_shape *s) {
 
 constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SMALL_M_GEMM |
                                GPTOSS_MOE_FLAG_LARGE_M_GEMM | GPTOSS_MOE_FLAG_FP4_MFMA |
-                               GPTOSS_MOE_FLAG_FP8_ACT;
+                               GPTOSS_MOE_FLAG_FP8_ACT | GPTOSS_MOE_FLAG_TILE_SWITCH;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -3040,7 +3102,7 @@ void launch_route_tb(int ee, const gptoss_moe_shape *s, const gptoss_moe_weights
 
 int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                  int T, const int32_t *fi, const uint16_t *fw, const Ptrs &p, hipStream_t st,
-                 int tile_rows, bool gather, Marks *mk = nullptr,
+                 int tile_rows, int big_rows, bool gather, Marks *mk = nullptr,
                  const uint16_t *rms_w = nullptr, uint16_t *t_out = nullptr) {
     int nthreads_ref = 1;
     while (nthreads_ref < s->n_experts) nthreads_ref <<= 1;
@@ -3068,7 +3130,7 @@ int launch_route(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const u
     G = G < 1 ? 1 : (G > 256 ? 256 : G);
     if (!gather) G = 1;
     hipLaunchKernelGGL(index_kernel, dim3(G, n_blk + 1), dim3(256), 0, st, p.hist, n_blk, p.slot_e,
-                       p.topk_w, x, T, s->top_k, E, s->hidden, bt, tile_rows, p.counts, p.offsets,
+                       p.topk_w, x, T, s->top_k, E, s->hidden, bt, tile_rows, big_rows, p.counts, p.offsets,
                        p.tiles, p.hdr, p.local_ids, p.row_token, p.row_w, p.row_slot,
                        gather ? p.xg : nullptr);
     if (mk) mk->mark(st);
@@ -3096,6 +3158,19 @@ GemmPath gemm_path(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T
     if (flags & GPTOSS_MOE_FLAG_LARGE_M_GEMM) return use_large_m(s, T, flags) ? PATH_LARGE_M : PATH_SMALL_M;
     if (w->packed != nullptr && !(flags & GPTOSS_MOE_FLAG_SMALL_M_GEMM)) return PATH_DIRECT;
     return use_large_m(s, T, flags) ? PATH_LARGE_M : PATH_SMALL_M;
+}
+
+// Per-expert tile switch (GPTOSS_MOE_FLAG_TILE_SWITCH): the expert count from
+// which the packed large-M GEMM takes an expert instead of the streamed GEMM;
+// INT_MAX when the switch is off, or when no expert can reach it (T below the
+// count) or the shape does not fit the large-M staging.
+int switch_rows(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, unsigned flags) {
+    if (!(flags & GPTOSS_MOE_FLAG_TILE_SWITCH) || gemm_path(s, w, T, flags) != PATH_DIRECT) return INT_MAX;
+    const long P = (long)T * s->top_k;
+    const bool fits = s->hidden >= 256 && s->intermediate >= 256 &&
+                      P / kLBM + s->n_experts / 8 + 1 <= kLMaxTiles;
+    if (!fits || T < GPTOSS_MOE_TILE_SWITCH_ROWS) return INT_MAX;
+    return GPTOSS_MOE_TILE_SWITCH_ROWS;
 }
 
 // Rows per tile of the tile list: the direct GEMM takes whole decode experts,
@@ -3163,17 +3238,23 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a1.alpha = s->swiglu_alpha;
     const GemmPath path = gemm_path(s, w, T, flags);
     const bool large = path == PATH_LARGE_M, direct = path == PATH_DIRECT, fp4 = path == PATH_FP4;
+    const int big = switch_rows(s, w, T, flags);
     const int terms = (flags & GPTOSS_MOE_FLAG_FP8_ACT) ? 1 : 2;
     const PackLayout PL = pack_layout(*s);
     GemmArgs a1x = a1;  // the direct GEMM reads x through the row map
     a1x.A = x;
     if (large)
-        hipLaunchKernelGGL(large_m_gemm_kernel<true>, dim3(cap), dim3(kLWaves * 64), 0, st, a1,
-                           p.counts, p.offsets, s->n_experts);
-    else if (direct)
+        hipLaunchKernelGGL((large_m_gemm_kernel<true, false>), dim3(cap), dim3(kLWaves * 64), 0, st, a1,
+                           p.counts, p.offsets, s->n_experts, LPacked{nullptr, nullptr, nullptr, 0});
+    else if (direct) {
         hipLaunchKernelGGL(stream_gemm_kernel<true>, dim3(cap), dim3(kSThreads), 0, st,
                            SArgs{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
                                  w->packed + PL.s1, p.row_token});
+        if (big < INT_MAX)  // the experts the streamed GEMM's tile list left out
+            hipLaunchKernelGGL((large_m_gemm_kernel<true, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a1x,
+                               p.counts, p.offsets, s->n_experts,
+                               LPacked{w->packed + PL.w1, w->packed + PL.s1, p.row_token, big});
+    }
     else if (fp4) {
         launch_quantize_act(x, T, H, terms, nullptr, p.xq, p.xqs, st);
         GemmArgs aq1 = a1;
@@ -3199,12 +3280,17 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     a2.N = H;
     a2.K = D;
     if (large)
-        hipLaunchKernelGGL(large_m_gemm_kernel<false>, dim3(cap), dim3(kLWaves * 64), 0, st, a2,
-                           p.counts, p.offsets, s->n_experts);
-    else if (direct)
+        hipLaunchKernelGGL((large_m_gemm_kernel<false, false>), dim3(cap), dim3(kLWaves * 64), 0, st, a2,
+                           p.counts, p.offsets, s->n_experts, LPacked{nullptr, nullptr, nullptr, 0});
+    else if (direct) {
         hipLaunchKernelGGL(stream_gemm_kernel<false>, dim3(cap), dim3(kSThreads), 0, st,
                            SArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
                                  w->packed + PL.s2, nullptr});
+        if (big < INT_MAX)
+            hipLaunchKernelGGL((large_m_gemm_kernel<false, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a2,
+                               p.counts, p.offsets, s->n_experts,
+                               LPacked{w->packed + PL.w2, w->packed + PL.s2, nullptr, big});
+    }
     else if (fp4) {
         // rows past offsets[E] (the live rows) are skipped
         launch_quantize_act(p.act, T * s->top_k, D, terms, p.offsets + s->n_experts, p.aq, p.aqs, st);
@@ -3332,7 +3418,8 @@ int gptoss_moe_route(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
     if (!x_norm || !aligned16(x_norm)) return GPTOSS_MOE_ERR_INVALID_ARG;
     const WsLayout L = ws_layout(*shape, max_tokens);
     return launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w,
-                        ws_ptrs(L, workspace), stream, gemm_tile_rows(shape, w, n_tokens, 0), false);
+                        ws_ptrs(L, workspace), stream, gemm_tile_rows(shape, w, n_tokens, 0), INT_MAX,
+                        false);
 }
 
 int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
@@ -3349,7 +3436,7 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
-                      gemm_tile_rows(shape, w, n_tokens, flags),
+                      gemm_tile_rows(shape, w, n_tokens, flags), switch_rows(shape, w, n_tokens, flags),
                       gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT);
     if (rc) return rc;
     return launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream);
@@ -3394,7 +3481,7 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
     const Ptrs p = ws_ptrs(L, workspace);
     mk.mark(stream);
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
-                      gemm_tile_rows(shape, w, n_tokens, flags),
+                      gemm_tile_rows(shape, w, n_tokens, flags), switch_rows(shape, w, n_tokens, flags),
                       gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT, &mk);
     if (!rc) rc = launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream, &mk);
     if (!rc) rc = hip_status(hipEventSynchronize(mk.ev[5]));
@@ -3433,7 +3520,7 @@ int gptoss_moe_layer(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
     rc = launch_route(shape, w, x, n_tokens, nullptr, nullptr, p, stream,
-                      gemm_tile_rows(shape, w, n_tokens, 0),
+                      gemm_tile_rows(shape, w, n_tokens, 0), INT_MAX,
                       gemm_path(shape, w, n_tokens, 0) < PATH_DIRECT, nullptr, rms_w, t_scratch);
     if (rc) return rc;
     return launch_experts(shape, w, t_scratch, x, n_tokens, GPTOSS_MOE_FLAG_RESIDUAL_ADD, L, p,

@@ -30,10 +30,14 @@ FLAG_SMALL_M_GEMM = 2
 FLAG_LARGE_M_GEMM = 4
 FLAG_FP4_MFMA = 8
 FLAG_FP8_ACT = 16
+FLAG_TILE_SWITCH = 32
 # "fp4": block-scaled FP4 MFMA on MXFP8 activations (hi + lo terms); "fp4_fp8":
 # the same with the hi term only.  Both need the packed_fp4 weights (pack_fp4()).
+# "switch": the packed path with the per-expert tile switch (experts of >= 128
+# rows on the large-M GEMM's 128-row tiles).
 _PATH_FLAGS = {"auto": 0, "small": FLAG_SMALL_M_GEMM, "large": FLAG_LARGE_M_GEMM,
-               "fp4": FLAG_FP4_MFMA, "fp4_fp8": FLAG_FP4_MFMA | FLAG_FP8_ACT}
+               "fp4": FLAG_FP4_MFMA, "fp4_fp8": FLAG_FP4_MFMA | FLAG_FP8_ACT,
+               "switch": FLAG_TILE_SWITCH}
 
 _ERRNAMES = {ERR_INVALID_ARG: "invalid argument", ERR_WORKSPACE: "workspace too small",
              ERR_HIP: "HIP error", ERR_UNSUPPORTED: "unsupported shape"}
@@ -310,7 +314,8 @@ class MoeLayer:
     def forward(self, x_norm, out=None, forced_i=None, forced_w=None, residual=False,
                 stream=None, path="auto"):
         """e_agg (or out + e_agg with residual=True) for bf16 rows x_norm [T][H].
-        path: "auto", "small" / "large" to force a grouped-GEMM path, or
+        path: "auto", "small" / "large" to force a grouped-GEMM path,
+        "switch" for the per-expert tile switch on packed weights, or
         "fp4" / "fp4_fp8" for the block-scaled FP4 MFMA variant."""
         import torch
         T = x_norm.shape[0]

@@ -60,6 +60,16 @@ extern "C" {
  * reference: 0 and +Inf).  Not combinable with SMALL_M / LARGE_M. */
 #define GPTOSS_MOE_FLAG_FP4_MFMA 8u
 #define GPTOSS_MOE_FLAG_FP8_ACT 16u
+/* Per-expert tile switch on the streamed path (packed weights): experts with
+ * at least GPTOSS_MOE_TILE_SWITCH_ROWS rows run on 128-row tiles with
+ * 32x32x16 MFMA (the large-M GEMM reading the packed weights; each weight
+ * fragment converted once per 128 rows), the others on the streamed GEMM's
+ * 64-row tiles.  The reference picks one tile shape for the whole call from
+ * the largest expert count (getp_run.cpp:2666).  Results are within the layer
+ * tolerance of the default, not bit-identical (another k order).  Needs
+ * hidden, intermediate >= 256; ignored without packed weights. */
+#define GPTOSS_MOE_FLAG_TILE_SWITCH 32u
+#define GPTOSS_MOE_TILE_SWITCH_ROWS 128
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {
