@@ -44,6 +44,8 @@ def parse():
                     help="only the C4 attention line (decode attention over the int8 KV cache)")
     ap.add_argument("--decoder-only", action="store_true",
                     help="only the C4 decode-step line (24 layers, 512 sequences)")
+    ap.add_argument("--c4-full", action="store_true",
+                    help="also the C4 attention and decode-step lines in a full run")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -561,15 +563,17 @@ def main():
             res["c4_moe_share"] = time_c4_moe_share(args, dev)
         except Exception as e:  # an extra line: report, never fail the headline
             res["c4_moe_share"] = {"error": f"{type(e).__name__}: {e}"}
-        try:
-            res["c4_attention"] = time_c4_attention(args, dev)
-        except Exception as e:  # an extra line: report, never fail the headline
-            res["c4_attention"] = {"error": f"{type(e).__name__}: {e}"}
-        torch.cuda.empty_cache()
-        try:
-            res["c4_decoder"] = time_c4_decoder(args, dev)
-        except Exception as e:  # an extra line: report, never fail the headline
-            res["c4_decoder"] = {"error": f"{type(e).__name__}: {e}"}
+        if args.c4_full:  # kernels that have not passed their GPU tests yet stay opt-in
+            torch.cuda.empty_cache()
+            try:
+                res["c4_attention"] = time_c4_attention(args, dev)
+            except Exception as e:  # an extra line: report, never fail the headline
+                res["c4_attention"] = {"error": f"{type(e).__name__}: {e}"}
+            torch.cuda.empty_cache()
+            try:
+                res["c4_decoder"] = time_c4_decoder(args, dev)
+            except Exception as e:
+                res["c4_decoder"] = {"error": f"{type(e).__name__}: {e}"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
     else:
