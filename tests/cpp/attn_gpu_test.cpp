@@ -1,5 +1,5 @@
 // C++ caller of the attention shim (gpt-oss_amd/csrc/attn_gpu_shim.hpp), run
-// by tests/test_zzz_gpu_attn.py: a mock of the reference's state with its
+// by tests/wip_gpu_attn.py: a mock of the reference's state with its
 // member names, T decode steps of every layer through
 // attention_cache_and_decode, then the last step again in two row ranges.
 //
