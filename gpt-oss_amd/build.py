@@ -28,7 +28,7 @@ ATTN_LIB = os.path.join(HERE, "libgptoss_attn.so")
 SHIM_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "moe_gpu_test.cpp")
 SHIM_TEST_BIN = os.path.join(HERE, "bin", "moe_gpu_test")
 # The same for the attention shim (csrc/attn_gpu_shim.hpp), run by
-# tests/test_zzz_gpu_attn.py.
+# tests/wip_gpu_attn.py.
 ATTN_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "attn_gpu_test.cpp")
 ATTN_TEST_BIN = os.path.join(HERE, "bin", "attn_gpu_test")
 

@@ -1,0 +1,191 @@
+"""The decode step's host code (gpt-oss_amd/decoder.py and gptoss_attn.KvCache)
+run on the CPU against a stand-in for the HIP library: every entry point of
+include/gptoss_attn.h and include/gptoss_decoder.h that the step calls is
+replaced by a function with the same C signature that reads and writes the
+same memory (the KV cache in the library's tile layout) and computes with
+the oracle.  The step must then reproduce the oracle's decode step
+(tests/decoder_ref.py): this checks the argument order, strides, cache
+offsets and control flow of the host code without a GPU.  The kernels
+themselves are checked by the GPU tests."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import decoder as dec
+import gptoss_attn as ga
+import gptoss_moe as gm
+import oracle
+from attn_layout import KV, from_logical, to_logical
+from decoder_ref import OracleDecoder
+from synth import f32_to_bf16
+
+
+def arr(ptr, n, dtype):
+    """numpy view of n elements at a host address."""
+    ct = {np.uint16: ctypes.c_uint16, np.int8: ctypes.c_int8, np.int32: ctypes.c_int32,
+          np.float32: ctypes.c_float}[dtype]
+    return np.ctypeslib.as_array((ct * n).from_address(ptr))
+
+
+class StandInLib:
+    """The library's C entry points over host memory, computed by the oracle."""
+
+    def __init__(self, real):
+        self.real = real  # host-only functions run as they are
+
+    def gptoss_attn_workspace_size(self, *a):
+        return self.real.gptoss_attn_workspace_size(*a)
+
+    def gptoss_dec_rope_table(self, *a):
+        return self.real.gptoss_dec_rope_table(*a)
+
+    def gptoss_attn_last_hip_error(self):
+        return 0
+
+    @staticmethod
+    def _layer(shape_p, cache_p, layer_p):
+        sh = ctypes.cast(shape_p, ctypes.POINTER(ga.Shape)).contents
+        ca = ctypes.cast(cache_p, ctypes.POINTER(ga.Cache)).contents
+        ly = ctypes.cast(layer_p, ctypes.POINTER(ga.Layer)).contents
+        return sh, ca, ly
+
+    def gptoss_attn_kv_update(self, shape_p, cache_p, layer_p, k, v, pos, n, stream):
+        sh, ca, ly = self._layer(shape_p, cache_p, layer_p)
+        pos = arr(pos, n, np.int32)
+        kk, vv = arr(k, n * KV, np.uint16).reshape(n, KV), arr(v, n * KV, np.uint16).reshape(n, KV)
+        kq, ks = oracle.kv_quantize_rows(kk)
+        vq, vs = oracle.kv_quantize_rows(vv)
+        ring = ly.layer_idx % 2 == 0 and sh.sliding_window > 0
+        for b in range(n):
+            p = int(pos[b])
+            if p < 0 or (not ring and p >= ly.cap):
+                continue
+            r = p % sh.sliding_window if ring else p
+            slab = lambda base, dt: arr(base + (b * ca.batch_kv_stride + ly.layer_kv_offset) * np.dtype(dt).itemsize,
+                                        ly.cap * KV, dt)
+            sk, sv = slab(ca.key_codes, np.int8), slab(ca.value_codes, np.int8)
+            lk, lv = to_logical(sk, sv, ly.cap)
+            lk[r], lv[r] = kq[b], vq[b]
+            nk, nv = from_logical(lk, lv)
+            sk[:], sv[:] = nk, nv
+            so = b * ca.batch_scale_stride + ly.layer_scale_offset + r
+            arr(ca.key_scales, so + 1, np.uint16)[so] = ks[b]
+            arr(ca.value_scales, so + 1, np.uint16)[so] = vs[b]
+            if ly.layer_idx % 2 == 1 and p < sh.keep:
+                off = (b * sh.n_layers + ly.layer_idx) * sh.keep * KV
+                bk = arr(ca.key_bf16 + 2 * off, sh.keep * KV, np.uint16)
+                bv = arr(ca.value_bf16 + 2 * off, sh.keep * KV, np.uint16)
+                lk, lv = to_logical(bk, bv, sh.keep)
+                lk[p], lv[p] = kk[b], vv[b]
+                bk[:], bv[:] = from_logical(lk, lv)
+        return 0
+
+    def gptoss_attn_decode(self, shape_p, cache_p, layer_p, q, sinks, pos, n, out, ws, ws_bytes, stream):
+        sh, ca, ly = self._layer(shape_p, cache_p, layer_p)
+        pos = arr(pos, n, np.int32).copy()
+        kq = np.zeros((n, ly.cap, KV), np.int8)
+        vq = np.zeros_like(kq)
+        ks = np.zeros((n, ly.cap), np.uint16)
+        vs = np.zeros_like(ks)
+        keep = sh.keep if ly.layer_idx % 2 == 1 else 0
+        kb = np.zeros((n, max(keep, 1), KV), np.uint16)
+        vb = np.zeros_like(kb)
+        for b in range(n):
+            o = b * ca.batch_kv_stride + ly.layer_kv_offset
+            kq[b], vq[b] = to_logical(arr(ca.key_codes + o, ly.cap * KV, np.int8),
+                                      arr(ca.value_codes + o, ly.cap * KV, np.int8), ly.cap)
+            so = b * ca.batch_scale_stride + ly.layer_scale_offset
+            ks[b] = arr(ca.key_scales + 2 * so, ly.cap, np.uint16)
+            vs[b] = arr(ca.value_scales + 2 * so, ly.cap, np.uint16)
+            if keep:
+                off = (b * sh.n_layers + ly.layer_idx) * keep * KV
+                kb[b], vb[b] = to_logical(arr(ca.key_bf16 + 2 * off, keep * KV, np.uint16),
+                                          arr(ca.value_bf16 + 2 * off, keep * KV, np.uint16), keep)
+        o32 = oracle.attn_decode(arr(q, n * 4096, np.uint16).reshape(n, 64, 64), kq, vq, ks, vs,
+                                 kb if keep else None, vb if keep else None, arr(sinks, 64, np.uint16),
+                                 pos, n_kv_heads=8, layer_idx=ly.layer_idx,
+                                 sliding_window=sh.sliding_window, keep=sh.keep,
+                                 prefix_rule=sh.prefix_rule)
+        arr(out, n * 4096, np.uint16)[:] = f32_to_bf16(o32).reshape(-1)
+        return 0
+
+    def gptoss_dec_embed(self, table, vocab, hidden, tokens, n, x, stream):
+        t = arr(tokens, n, np.int32)
+        arr(x, n * hidden, np.uint16).reshape(n, hidden)[:] = arr(table, vocab * hidden, np.uint16).reshape(vocab, hidden)[t]
+        return 0
+
+    def gptoss_dec_qkv_rope(self, qkv, bias, cos, sin, n_pos, pos, n, q, k, v, stream):
+        W = 5120
+        rq, rk, rv = oracle.qkv_bias_rope(arr(qkv, n * W, np.uint16).reshape(n, W), arr(bias, W, np.uint16),
+                                          arr(cos, n_pos * 32, np.float32).reshape(n_pos, 32),
+                                          arr(sin, n_pos * 32, np.float32).reshape(n_pos, 32),
+                                          arr(pos, n, np.int32))
+        arr(q, n * 4096, np.uint16)[:] = rq.reshape(-1)
+        arr(k, n * 512, np.uint16)[:] = rk.reshape(-1)
+        arr(v, n * 512, np.uint16)[:] = rv.reshape(-1)
+        return 0
+
+    def gptoss_dec_bias_residual(self, x, proj, bias, n, hidden, stream):
+        xv = arr(x, n * hidden, np.uint16).reshape(n, hidden)
+        xv[:] = oracle.bias_residual(xv, arr(proj, n * hidden, np.uint16).reshape(n, hidden),
+                                     arr(bias, hidden, np.uint16))
+        return 0
+
+    def gptoss_dec_argmax(self, logits, n, cols, out, stream):
+        arr(out, n, np.int32)[:] = oracle.argmax_bf16(arr(logits, n * cols, np.uint16).reshape(n, cols))
+        return 0
+
+
+class StandInMoe:
+    """MoeLayer.layer (gptoss_moe_layer): x += MoE(RMSNorm(x)), by the oracle."""
+
+    def __init__(self, d):
+        self.d = d
+
+    def layer(self, x, rms_w, t_scratch=None, stream=None):
+        xv = x.numpy().view(np.uint16)
+        t = oracle.rmsnorm(xv, rms_w.numpy().view(np.uint16))
+        e = oracle.moe_forward(self.d, x_norm=t, forced=False)["e_agg"]
+        xv[:] = oracle.residual_add(xv, e)
+        return x
+
+
+def test_decode_step_host_code_on_the_cpu(monkeypatch):
+    cfg = dec.DecoderConfig(hidden=256, intermediate=256, n_experts=8, top_k=4, n_layers=2, vocab=512,
+                            max_ctx=64, sliding_window=32, keep=16, prefix_rule=ga.PREFIX_MIXED)
+    B, steps = 3, 40
+    stand_in = StandInLib(ga.load_library())
+    monkeypatch.setattr(ga, "_lib", stand_in)
+    monkeypatch.setattr(ga, "_stream", lambda stream=None: 0)
+
+    def rmsnorm(x, weight, out=None, stream=None):
+        r = oracle.rmsnorm(x.numpy().view(np.uint16), weight.numpy().view(np.uint16))
+        out.numpy().view(np.uint16)[:] = r
+        return out
+    monkeypatch.setattr(gm, "rmsnorm", rmsnorm)
+    w, moe = dec.make_host_weights(cfg)
+    up = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16))
+    dw = {k: ([up(a) for a in v] if isinstance(v, list) else up(v)) for k, v in w.items()}
+    model = dec.Decoder(cfg, B, dw, [StandInMoe(d) for d in moe], device="cpu")
+    ref = OracleDecoder(cfg, B, w, moe)
+    rng = np.random.default_rng(3)
+    for s in range(steps):
+        tokens = rng.integers(0, cfg.vocab, B).astype(np.int32)
+        pos = np.full(B, s, np.int32)
+        nxt = model.step(torch.from_numpy(tokens), torch.from_numpy(pos))
+        logits, ref_next = ref.step(tokens, pos)
+    got = model.logits.view(torch.int16).numpy().view(np.uint16)
+    # torch's CPU bf16 GEMM accumulates in fp32, the oracle in double: the
+    # projections differ by at most a rounding, the rest is the same arithmetic
+    from parity import compare
+    m = compare(got, logits)
+    assert m["rel_l2"] <= 2e-2, m
+    # the caches the host code addressed hold what the oracle's caches hold
+    for l in range(cfg.n_layers):
+        kq, vq, ks, vs, kb, vb = model.kv.layer_slabs(l)
+        for b in range(B):
+            lk, _ = to_logical(kq[b], vq[b], model.kv.caps[l])
+            agree = (lk == ref.kq[l][b]).mean()
+            assert agree > 0.98, (l, b, agree)
