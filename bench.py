@@ -386,9 +386,23 @@ def time_c4_decoder(args, dev):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     nxt = model.next.cpu()
+    graph_ms = None
+    try:  # the same step as one HIP graph (launch overhead of ~200 kernels and 73 GEMMs)
+        graph = dec.capture_step(model, tokens, pos)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph_ms = round(e0.elapsed_time(e1) / steps, 4)
+    except Exception as e:  # report, never fail the line
+        graph_ms = f"{type(e).__name__}: {e}"
     return {"workload": "c4 decode step: 20B shape, 24 layers, vocabulary 201088, 512 sequences at "
                         "position 1023 (window 128 on even layers, 128 bf16 tokens on odd layers)",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1), "steps": steps,
+            "graph_ms_per_step": graph_ms,
             "next_tokens_in_range": bool(((nxt >= 0) & (nxt < cfg.vocab)).all()),
             "note": "each timed step rewrites position 1023's cache rows and attends over 1024 "
                     "positions; dense projections on torch.matmul (hipBLASLt)"}

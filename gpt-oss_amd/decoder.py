@@ -143,6 +143,24 @@ class Decoder:
         return self.next
 
 
+def capture_step(model: Decoder, tokens, pos):
+    """A HIP graph of one model.step(tokens, pos) (a torch.cuda.CUDAGraph;
+    .replay() reruns the step on whatever tokens and pos then hold).  Every
+    call of the step allocates nothing in this package's libraries, issues no
+    memset and does not synchronise; the GEMMs take their workspace from the
+    graph's pool.  One warm-up step runs on a side stream first."""
+    import torch
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        model.step(tokens, pos)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model.step(tokens, pos)
+    return graph
+
+
 def make_host_weights(cfg: DecoderConfig, seed: int = 0xDEC0DE):
     """Random-init weights of the architecture as numpy (bf16 bits; MoE
     layers as synth.MoeData), for tests at small shapes."""

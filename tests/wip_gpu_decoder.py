@@ -104,3 +104,27 @@ def test_decoder_end_to_end(model):
     m = parity.compare(got, want)
     parity.RECORD.append({"what": "decoder end to end, last step", **{k: m[k] for k in ("max_abs", "max_abs_norm", "rel_l2", "frac_exact")}})
     assert m["finite"] and m["rel_l2"] <= 5e-2, m
+
+
+def test_decoder_graph_replays_match_eager(model):
+    """The whole step captured as a HIP graph: each replay, with eager steps
+    of other positions in between, gives the eager step's logits bit for bit
+    (the cache update at the replayed position rewrites the same rows)."""
+    w, moe = model
+    gpu = dec.from_host(CFG, B, w, moe)
+    rng = np.random.default_rng(13)
+    for s in range(10):
+        gpu.step(torch.from_numpy(rng.integers(0, CFG.vocab, B).astype(np.int32)).cuda(),
+                 torch.full((B,), s, dtype=torch.int32, device="cuda"))
+    tokens = torch.from_numpy(rng.integers(0, CFG.vocab, B).astype(np.int32)).cuda()
+    pos = torch.full((B,), 10, dtype=torch.int32, device="cuda")
+    graph = dec.capture_step(gpu, tokens, pos)
+    gpu.step(tokens, pos)
+    want = gpu.logits.clone()
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gpu.logits, want), f"replay {r}"
+        # eager work of another position between replays (rows past 10 are not attended at 10)
+        gpu.step(tokens, torch.full((B,), 11 + r, dtype=torch.int32, device="cuda"))
+        torch.cuda.synchronize()
