@@ -1,9 +1,11 @@
-// attn_gpu_shim.hpp — steps 5 and 6 of the reference's attention_gpu on this
-// library.
+// attn_gpu_shim.hpp — steps 5 and 6 of the reference's attention_gpu_120b /
+// attention_gpu on this library.
 //
-// Drop-in for the block of attention_gpu (getp-csrc/getp_run.cpp:2311-2470)
-// that updates the KV cache (quantize_kv_cache_kernel_int8 / _bf16) and runs
-// the fused flash-decoding kernel: `attention_cache_and_decode(gpu_t,
+// Drop-in for the block of attention_gpu_120b (getp-csrc/getp_run.cpp:
+// 2311-2470: quantize_kv_cache_kernel_int8 / _bf16 and the int8 flash-decoding
+// kernels) or of attention_gpu (:2096-2160, the 20B path: update_kv_cache_kernel
+// and ..._full_bf16kv_okay on the bf16 cache) that updates the KV cache and
+// runs the fused flash-decoding kernel: `attention_cache_and_decode(gpu_t,
 // layer_idx, batch_size, row_offset, stream)` does both for rows
 // [row_offset, row_offset + batch_size) of the run state, reading the query,
 // key and value that steps 1-4 left in state.{q, k, v} and writing state.tb,
@@ -14,7 +16,7 @@
 // config.{n_layers, n_attn_heads, n_kv_heads, head_dim, sliding_window},
 // weights.attn_sinks, state.{q, k, v, tb, positions, key_cache, value_cache,
 // key_cache_scales, value_cache_scales, key_cache_recent_bf16,
-// value_cache_recent_bf16}.
+// value_cache_recent_bf16, key_cache_bf16, value_cache_bf16}.
 //
 // The caches keep the reference's allocations and per-layer offsets
 // (getp_run.cpp:2195-2230); the byte order inside each 16-row block is this
@@ -57,15 +59,18 @@ inline void fail(const char *what, int rc) {
 
 // Warm-up: the model's shape, the reference's compile-time MAX_SEQ_LEN,
 // SW_WINDOW and KV_BF16_KEEP_TOKENS, the token source rule of the kept
-// tokens (GPTOSS_ATTN_PREFIX_*), and a workspace for up to max_batch
+// tokens (GPTOSS_ATTN_PREFIX_*), the cache kind (GPTOSS_ATTN_CACHE_INT8 for
+// attention_gpu_120b's caches, GPTOSS_ATTN_CACHE_BF16 for attention_gpu's
+// key_cache_bf16 / value_cache_bf16), and a workspace for up to max_batch
 // sequences.  Allocates (warm-up only).
 template <class GPUTransformer>
 void attn_gpu_init(GPUTransformer *gpu_t, int max_batch, int max_seq_len, int sw_window, int keep,
-                   int prefix_rule) {
+                   int prefix_rule, int cache_kind = GPTOSS_ATTN_CACHE_INT8) {
     auto *p = &gpu_t->config;
     State &S = state();
     S.shape = gptoss_attn_shape{p->n_attn_heads, p->n_kv_heads, p->head_dim, p->n_layers,
-                                p->sliding_window > 0 ? sw_window : 0, keep, prefix_rule};
+                                p->sliding_window > 0 ? sw_window : 0,
+                                cache_kind == GPTOSS_ATTN_CACHE_BF16 ? 0 : keep, prefix_rule, cache_kind};
     S.max_seq_len = max_seq_len;
     S.sw_window = sw_window;
     S.ws_bytes = gptoss_attn_workspace_size(&S.shape, max_seq_len, max_batch);
@@ -75,7 +80,8 @@ void attn_gpu_init(GPUTransformer *gpu_t, int max_batch, int max_seq_len, int sw
 
 }  // namespace gptoss_attn_shim
 
-// Steps 5) and 6) of attention_gpu (getp_run.cpp:2311-2470).
+// Steps 5) and 6) of attention_gpu_120b (getp_run.cpp:2311-2470) or
+// attention_gpu (:2096-2160).
 template <class GPUTransformer>
 void attention_cache_and_decode(GPUTransformer *gpu_t, int layer_idx, int batch_size, int row_offset,
                                 hipStream_t sAttn) {
@@ -102,10 +108,15 @@ void attention_cache_and_decode(GPUTransformer *gpu_t, int layer_idx, int batch_
     const size_t kv_slice = layers_capacity * (size_t)KV;
     const size_t recent_slice = (size_t)p->n_layers * (size_t)S.shape.keep * (size_t)KV;
     gptoss_attn_cache cache{};
-    cache.key_codes = reinterpret_cast<int8_t *>(s->key_cache) + (size_t)row_offset * kv_slice;
-    cache.value_codes = reinterpret_cast<int8_t *>(s->value_cache) + (size_t)row_offset * kv_slice;
-    cache.key_scales = reinterpret_cast<uint16_t *>(s->key_cache_scales) + (size_t)row_offset * layers_capacity;
-    cache.value_scales = reinterpret_cast<uint16_t *>(s->value_cache_scales) + (size_t)row_offset * layers_capacity;
+    if (S.shape.cache_kind == GPTOSS_ATTN_CACHE_BF16) {  // attention_gpu's bf16 rows (getp_run.cpp:2052-2053)
+        cache.key_codes = reinterpret_cast<int8_t *>(s->key_cache_bf16 + (size_t)row_offset * kv_slice);
+        cache.value_codes = reinterpret_cast<int8_t *>(s->value_cache_bf16 + (size_t)row_offset * kv_slice);
+    } else {
+        cache.key_codes = reinterpret_cast<int8_t *>(s->key_cache) + (size_t)row_offset * kv_slice;
+        cache.value_codes = reinterpret_cast<int8_t *>(s->value_cache) + (size_t)row_offset * kv_slice;
+        cache.key_scales = reinterpret_cast<uint16_t *>(s->key_cache_scales) + (size_t)row_offset * layers_capacity;
+        cache.value_scales = reinterpret_cast<uint16_t *>(s->value_cache_scales) + (size_t)row_offset * layers_capacity;
+    }
     if (S.shape.keep > 0) {
         cache.key_bf16 = reinterpret_cast<uint16_t *>(s->key_cache_recent_bf16) + (size_t)row_offset * recent_slice;
         cache.value_bf16 = reinterpret_cast<uint16_t *>(s->value_cache_recent_bf16) + (size_t)row_offset * recent_slice;

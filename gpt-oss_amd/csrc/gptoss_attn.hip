@@ -1,7 +1,9 @@
-// gptoss_attn.hip — decode attention over an int8 KV cache for gfx950.
+// gptoss_attn.hip — decode attention over an int8 (or bf16) KV cache for
+// gfx950.
 //
-// Two kernels per layer and decode step, as in the reference's attention_gpu
-// (getp-csrc/getp_run.cpp:2311-2470):
+// Two kernels per layer and decode step, as in the reference's
+// attention_gpu_120b (getp-csrc/getp_run.cpp:2311-2470; the bf16-cache kind
+// is attention_gpu's, :2096-2160):
 //   kv_update_kernel   the current token's K/V row -> int8 codes + fp16 scale
 //                      (+ a bf16 copy of odd layers' first `keep` tokens)
 //                      (attention.hpp:536-720);
@@ -138,7 +140,7 @@ struct KvArgs {
     size_t bks, bss, lko, lso;
     const uint16_t *k, *v;
     const int32_t *pos;
-    int cap, window, ring, odd, keep, n_layers, layer;
+    int cap, window, ring, odd, keep, n_layers, layer, bf16cache;
 };
 
 __device__ inline int v_tile_off(int r, int d) {  // value element (row r % 16, dim d) in a tile
@@ -153,6 +155,15 @@ __global__ __launch_bounds__(64) void kv_update_kernel(KvArgs a) {
     const int kvh = l >> 3, d0 = 8 * (l & 7);
     const u32x4 kr = ld16(a.k + (size_t)b * kKvDim + 8 * l);
     const u32x4 vr = ld16(a.v + (size_t)b * kKvDim + 8 * l);
+    if (a.bf16cache) {  // the rows themselves (update_kv_cache_kernel, attention.hpp:756-778)
+        uint16_t *kc = reinterpret_cast<uint16_t *>(a.kc), *vc = reinterpret_cast<uint16_t *>(a.vc);
+        const size_t tile = (size_t)b * a.bks + a.lko + (size_t)((r >> 4) * kKvHeads + kvh) * kTile;
+        *(u32x4 *)(kc + tile + (r & 15) * 64 + d0) = kr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            vc[tile + v_tile_off(r, d0 + j)] = (uint16_t)(j & 1 ? vr[j >> 1] >> 16 : vr[j >> 1] & 0xffffu);
+        return;
+    }
     float kf[8], vf[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -193,7 +204,8 @@ __global__ __launch_bounds__(64) void kv_update_kernel(KvArgs a) {
         a.vs[so] = f2h(safe_v / 127.f);
     }
     if (a.odd && pos < a.keep) {  // the bf16 copy (attention.hpp:630-652)
-        const size_t slab = ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
+        const size_t slab = a.bf16cache ? (size_t)b * a.bks + a.lko  // the bf16 cache's layer
+                                        : ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
         const size_t bt = slab + (size_t)((pos >> 4) * kKvHeads + kvh) * kTile;
         *(u32x4 *)(a.kb + bt + (pos & 15) * 64 + d0) = kr;
 #pragma unroll
@@ -212,7 +224,7 @@ struct DecArgs {
     const int32_t *pos;
     uint16_t *out;
     float *ws;
-    int cap, window, ring, odd, keep, rule, n_layers, layer, splits;
+    int cap, window, ring, odd, keep, rule, n_layers, layer, splits, bf16cache;
 };
 
 struct RawI8 {        // an int8 block as loaded: key tile, value tile, scales of tokens 4g..4g+3
@@ -405,9 +417,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3, 8))) void
     }
     const int nvalid = a.ring ? min(pos + 1, a.window) : pos + 1;
     const int nblk = (nvalid + 15) >> 4;
-    int nb16 = 0;
-    if (a.odd && a.keep > 0) nb16 = a.rule == GPTOSS_ATTN_PREFIX_REFERENCE ? (pos < a.keep ? nblk : 0)
-                                                                         : min(nblk, a.keep >> 4);
+    int nb16 = 0;  // leading blocks read as bf16 rows
+    if (a.bf16cache) nb16 = nblk;
+    else if (a.odd && a.keep > 0) nb16 = a.rule == GPTOSS_ATTN_PREFIX_REFERENCE ? (pos < a.keep ? nblk : 0)
+                                                                              : min(nblk, a.keep >> 4);
     const int blk0 = (int)((int64_t)nblk * s / S), blk1 = (int)((int64_t)nblk * (s + 1) / S);
 
     // The query of head c (heads 8..15 of the instruction are zero), dims
@@ -608,7 +621,8 @@ bool shape_ok(const gptoss_attn_shape *s) {
     return s && s->n_heads == kKvHeads * kGqa && s->n_kv_heads == kKvHeads && s->head_dim == kHd &&
            s->n_layers >= 1 && s->sliding_window >= 0 && s->sliding_window % 16 == 0 &&
            s->keep >= 0 && s->keep % 16 == 0 &&
-           (s->prefix_rule == GPTOSS_ATTN_PREFIX_REFERENCE || s->prefix_rule == GPTOSS_ATTN_PREFIX_MIXED);
+           (s->prefix_rule == GPTOSS_ATTN_PREFIX_REFERENCE || s->prefix_rule == GPTOSS_ATTN_PREFIX_MIXED) &&
+           (s->cache_kind == GPTOSS_ATTN_CACHE_INT8 || s->cache_kind == GPTOSS_ATTN_CACHE_BF16);
 }
 
 bool ring_layer(const gptoss_attn_shape *s, const gptoss_attn_layer *l) {
@@ -628,9 +642,10 @@ bool layer_ok(const gptoss_attn_shape *s, const gptoss_attn_cache *c, const gpto
     if (c->batch_kv_stride % kTile || c->batch_scale_stride % 16) return false;
     if (c->batch_kv_stride < l->layer_kv_offset + (size_t)l->cap * kKvDim) return false;
     if (c->batch_scale_stride < l->layer_scale_offset + (size_t)l->cap) return false;
-    if (!c->key_codes || !c->value_codes || !c->key_scales || !c->value_scales) return false;
-    if (!aligned(c->key_codes, 16) || !aligned(c->value_codes, 16) || !aligned(c->key_scales, 8) ||
-        !aligned(c->value_scales, 8))
+    if (!c->key_codes || !c->value_codes || !aligned(c->key_codes, 16) || !aligned(c->value_codes, 16))
+        return false;
+    if (s->cache_kind == GPTOSS_ATTN_CACHE_BF16) return true;  // rows only: no scales, no kept rows
+    if (!c->key_scales || !c->value_scales || !aligned(c->key_scales, 8) || !aligned(c->value_scales, 8))
         return false;
     if ((l->layer_idx & 1) && s->keep > 0) {
         if (s->keep > l->cap) return false;
@@ -641,11 +656,12 @@ bool layer_ok(const gptoss_attn_shape *s, const gptoss_attn_cache *c, const gpto
 }
 
 void fill_common(const gptoss_attn_shape *s, const gptoss_attn_layer *l, int &window, int &ring,
-                 int &odd, int &keep) {
+                 int &odd, int &keep, int &bf16cache) {
     ring = ring_layer(s, l) ? 1 : 0;
     window = s->sliding_window;
     odd = l->layer_idx & 1;
-    keep = odd ? s->keep : 0;
+    bf16cache = s->cache_kind == GPTOSS_ATTN_CACHE_BF16 ? 1 : 0;
+    keep = odd && !bf16cache ? s->keep : 0;
 }
 
 int splits_for(const gptoss_attn_shape *s, int rows, int n_seqs) {
@@ -682,7 +698,7 @@ int gptoss_attn_kv_update(const gptoss_attn_shape *shape, const gptoss_attn_cach
     a.v = v;
     a.pos = pos;
     a.cap = layer->cap;
-    fill_common(shape, layer, a.window, a.ring, a.odd, a.keep);
+    fill_common(shape, layer, a.window, a.ring, a.odd, a.keep, a.bf16cache);
     a.n_layers = shape->n_layers;
     a.layer = layer->layer_idx;
     hipLaunchKernelGGL(kv_update_kernel, dim3(n_seqs), dim3(64), 0, stream, a);
@@ -723,8 +739,12 @@ int gptoss_attn_decode(const gptoss_attn_shape *shape, const gptoss_attn_cache *
     a.pos = pos;
     a.out = out;
     a.cap = layer->cap;
-    fill_common(shape, layer, a.window, a.ring, a.odd, a.keep);
+    fill_common(shape, layer, a.window, a.ring, a.odd, a.keep, a.bf16cache);
     a.rule = shape->prefix_rule;
+    if (a.bf16cache) {  // the blocks are the cache's own bf16 rows
+        a.kb = reinterpret_cast<const uint16_t *>(cache->key_codes);
+        a.vb = reinterpret_cast<const uint16_t *>(cache->value_codes);
+    }
     a.n_layers = shape->n_layers;
     a.layer = layer->layer_idx;
     int S = splits_for(shape, layer_rows(shape, layer), n_seqs);

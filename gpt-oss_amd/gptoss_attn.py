@@ -6,8 +6,11 @@ csrc/gptoss_attn.hip).
 :443-486) for `n_seqs` sequences and every layer, with the reference's
 strides: per sequence, even layers hold `sliding_window` rows and odd layers
 `max_ctx` rows of kv_dim int8 codes, one fp16 scale per row, and odd layers'
-first `keep` tokens again in bf16.  `kv_update` and `decode` are the two
-kernel launches of attention_gpu (getp_run.cpp:2326-2470).  torch tensors
+first `keep` tokens again in bf16 (attention_gpu_120b); with
+cache_kind=CACHE_BF16 the rows are the bf16 K/V themselves (key_cache_bf16,
+the 20B model's attention_gpu).  `kv_update` and `decode` are the two kernel
+launches of attention_gpu_120b (getp_run.cpp:2326-2470) or attention_gpu
+(:2096-2160).  torch tensors
 serve as device memory only; there is no fallback: a missing library or a
 failed call raises.
 """
@@ -25,6 +28,8 @@ ERR_WORKSPACE = -2
 ERR_HIP = -3
 PREFIX_REFERENCE = 0
 PREFIX_MIXED = 1
+CACHE_INT8 = 0   # codes + fp16 scales (+ bf16-kept rows): the reference's 120B path
+CACHE_BF16 = 1   # bf16 rows: the reference's 20B path
 N_HEADS, N_KV_HEADS, HEAD_DIM = 64, 8, 64
 KV_DIM = N_KV_HEADS * HEAD_DIM
 
@@ -37,7 +42,7 @@ class AttnError(RuntimeError):
 
 class Shape(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("n_heads", "n_kv_heads", "head_dim", "n_layers",
-                                            "sliding_window", "keep", "prefix_rule")]
+                                            "sliding_window", "keep", "prefix_rule", "cache_kind")]
 
 
 class Cache(ctypes.Structure):
@@ -105,19 +110,24 @@ def layer_caps(n_layers: int, sliding_window: int, max_ctx: int):
 
 class KvCache:
     def __init__(self, n_seqs: int, n_layers: int, max_ctx: int, sliding_window: int = 128,
-                 keep: int = 16, prefix_rule: int = PREFIX_REFERENCE, device="cuda"):
+                 keep: int = 16, prefix_rule: int = PREFIX_REFERENCE, device="cuda",
+                 cache_kind: int = CACHE_INT8):
         import torch
         if max_ctx % 16 or sliding_window % 16 or keep % 16:
             raise ValueError("max_ctx, sliding_window and keep must be multiples of 16")
+        if cache_kind == CACHE_BF16:
+            keep = 0  # the rows are bf16 already
         self.lib = load_library()
         self.n_seqs, self.n_layers, self.max_ctx = n_seqs, n_layers, max_ctx
+        self.cache_kind = cache_kind
         self.shape = Shape(N_HEADS, N_KV_HEADS, HEAD_DIM, n_layers, sliding_window, keep,
-                           prefix_rule)
+                           prefix_rule, cache_kind)
         self.caps = layer_caps(n_layers, sliding_window, max_ctx)
         self.offsets = [sum(self.caps[:l]) for l in range(n_layers)]
         rows = sum(self.caps)
         self.rows = rows
-        self.key_codes = torch.zeros(n_seqs * rows * KV_DIM, dtype=torch.int8, device=device)
+        code_dtype = torch.int16 if cache_kind == CACHE_BF16 else torch.int8
+        self.key_codes = torch.zeros(n_seqs * rows * KV_DIM, dtype=code_dtype, device=device)
         self.value_codes = torch.zeros_like(self.key_codes)
         self.key_scales = torch.zeros(n_seqs * rows, dtype=torch.int16, device=device)
         self.value_scales = torch.zeros_like(self.key_scales)
@@ -178,6 +188,9 @@ class KvCache:
         vb = self.value_bf16[:self.n_seqs * self.n_layers * keep * KV_DIM].view(
             self.n_seqs, self.n_layers, keep * KV_DIM)[:, l] if keep else None
         cpu = lambda t: None if t is None else t.cpu().numpy()
+        if self.cache_kind == CACHE_BF16:
+            kc, vc = cpu(kc).view(np.uint16), cpu(vc).view(np.uint16)
+            return kc, vc, None, None, None, None
         return (cpu(kc), cpu(vc), cpu(ks).view(np.uint16), cpu(vs).view(np.uint16),
                 None if kb is None else cpu(kb).view(np.uint16),
                 None if vb is None else cpu(vb).view(np.uint16))

@@ -7,19 +7,26 @@
  * returns an int status (0 = ok, negative = error), never exits, allocates
  * nothing and does not synchronise the host.
  *
- * Scope (what the reference's GPU decode path computes per layer,
- * getp-csrc/getp_run.cpp:2311-2470): the KV-cache update of the current
- * token (quantize_kv_cache_kernel_{int8,bf16}, kernels/attention.hpp:536-720)
- * and the attention of one query token per sequence with learned sinks, a
- * sliding window on even layers and GQA (flashdecoding_fused_fastmerge_
- * nostage_1warp8q_bf16q_bf16out{,_bf16kv}, kernels/attention_mfma.hpp:
- * 1113-1460).  gpt-oss shapes only: 64 query heads, 8 KV heads, head_dim 64.
+ * Scope (what the reference's GPU decode paths compute per layer): the
+ * KV-cache update of the current token and the attention of one query token
+ * per sequence with learned sinks, a sliding window on even layers and GQA,
+ * over either cache the reference keeps:
+ *   int8 (attention_gpu_120b, getp-csrc/getp_run.cpp:2181-2481):
+ *     quantize_kv_cache_kernel_{int8,bf16} (kernels/attention.hpp:536-720)
+ *     and flashdecoding_fused_fastmerge_nostage_1warp8q_bf16q_bf16out
+ *     {,_bf16kv} (kernels/attention_mfma.hpp:1113-1460);
+ *   bf16 (attention_gpu, getp_run.cpp:2008-2180, the 20B model):
+ *     update_kv_cache_kernel (attention.hpp:756-778) and
+ *     flashdecoding_fused_fastmerge_nostage_1warp8q_bf16q_bf16out_full_bf16kv
+ *     _okay (attention_mfma.hpp:1679-1900).
+ * gpt-oss shapes only: 64 query heads, 8 KV heads, head_dim 64.
  *
  * Cache memory.  The allocations, strides and per-layer offsets are the
  * reference's (GPURunState.key_cache / value_cache / key_cache_scales /
  * value_cache_scales / key_cache_recent_bf16 / value_cache_recent_bf16,
  * getp_run.cpp:104-112, :443-486): per sequence b, layer l owns `cap` rows of
- * kv_dim = 512 int8 values at element offset
+ * kv_dim = 512 values (int8 codes, or bf16 with GPTOSS_ATTN_CACHE_BF16) at
+ * element offset
  *     b * batch_kv_stride + layer_kv_offset,
  * one fp16 scale per row at  b * batch_scale_stride + layer_scale_offset,
  * and (odd layers, keep > 0) `keep` bf16 rows at
@@ -65,6 +72,13 @@ extern "C" {
 #define GPTOSS_ATTN_PREFIX_REFERENCE 0
 #define GPTOSS_ATTN_PREFIX_MIXED 1
 
+/* Cache kind.  INT8: codes + fp16 scales per row (+ the bf16-kept rows of
+ * odd layers).  BF16: the rows themselves in bf16 (key_codes / value_codes
+ * then point to uint16_t bf16 elements, same element offsets and tile
+ * order; scales, keep and the bf16-kept rows are not used). */
+#define GPTOSS_ATTN_CACHE_INT8 0
+#define GPTOSS_ATTN_CACHE_BF16 1
+
 /* Model shape (run.cpp Config fields; getp_run.cpp's compile-time
  * SW_WINDOW and KV_BF16_KEEP_TOKENS). */
 typedef struct gptoss_attn_shape {
@@ -75,11 +89,13 @@ typedef struct gptoss_attn_shape {
     int sliding_window;  /* Config.sliding_window (ring rows of even layers): 0 or a multiple of 16 */
     int keep;            /* bf16-kept tokens of odd layers: 0 or a multiple of 16 */
     int prefix_rule;     /* GPTOSS_ATTN_PREFIX_* */
+    int cache_kind;      /* GPTOSS_ATTN_CACHE_* */
 } gptoss_attn_shape;
 
 /* The caches of all sequences and layers (GPURunState fields).  Device
  * pointers; key/value codes 16-byte aligned, scales 8-byte aligned, bf16
- * rows 16-byte aligned (NULL when keep == 0). */
+ * rows 16-byte aligned (NULL when keep == 0).  With GPTOSS_ATTN_CACHE_BF16
+ * only key_codes / value_codes (bf16 elements) are read. */
 typedef struct gptoss_attn_cache {
     int8_t *key_codes;
     int8_t *value_codes;
@@ -103,11 +119,13 @@ typedef struct gptoss_attn_layer {
 
 /* KV-cache update of the current token of n_seqs sequences
  * (quantize_kv_cache_kernel_int8 / _bf16, attention.hpp:536-720, launched at
- * getp_run.cpp:2326-2360): k, v bf16 [n_seqs][n_kv_heads * head_dim] (after
- * RoPE), pos int32 [n_seqs] (device).  Writes each row's int8 codes with an
- * fp16 scale max(max|x|, 1e-6) / 127 and codes rint(x * 127 / that max)
- * clamped to +-127; on odd layers with pos < keep also the bf16 row.  A
- * sequence with pos < 0, or pos >= cap where rows are not a ring, is skipped
+ * getp_run.cpp:2326-2360; with a bf16 cache update_kv_cache_kernel,
+ * attention.hpp:756-778, launched at getp_run.cpp:2096-2105): k, v bf16
+ * [n_seqs][n_kv_heads * head_dim] (after RoPE), pos int32 [n_seqs] (device).
+ * int8: writes each row's codes with an fp16 scale max(max|x|, 1e-6) / 127
+ * and codes rint(x * 127 / that max) clamped to +-127; on odd layers with
+ * pos < keep also the bf16 row.  bf16: writes the row.  A sequence with
+ * pos < 0, or pos >= cap where rows are not a ring, is skipped
  * (attention.hpp:557-558). */
 int gptoss_attn_kv_update(const gptoss_attn_shape *shape, const gptoss_attn_cache *cache,
                           const gptoss_attn_layer *layer, const uint16_t *k, const uint16_t *v,
@@ -121,7 +139,9 @@ size_t gptoss_attn_workspace_size(const gptoss_attn_shape *shape, int cap, int n
 
 /* Decode attention (flashdecoding_fused_fastmerge_nostage_1warp8q_bf16q_
  * bf16out{,_bf16kv}, attention_mfma.hpp:1113-1460, launched at
- * getp_run.cpp:2362-2470) for the token at pos[b] of each sequence, whose
+ * getp_run.cpp:2362-2470; with a bf16 cache ..._full_bf16kv_okay,
+ * attention_mfma.hpp:1679-1900, launched at getp_run.cpp:2107-2135) for the
+ * token at pos[b] of each sequence, whose
  * row gptoss_attn_kv_update has written:
  *     out[b][h] = sum_t softmax_t(q[b][h] . k_t / sqrt(64) | sink[h]) v_t
  * over t in [max(0, pos - sliding_window + 1), pos] on even layers (when

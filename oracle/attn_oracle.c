@@ -35,7 +35,11 @@
  *
  * Caches are in the reference's logical layout: kq/vq [B][cap][kv_dim] int8,
  * ks/vs [B][cap] fp16 bit patterns, kb/vb [B][keep][kv_dim] bf16 bit
- * patterns; q [B][n_heads][head_dim] bf16; sinks [n_heads] bf16.
+ * patterns; q [B][n_heads][head_dim] bf16; sinks [n_heads] bf16.  With
+ * cache_bf16 (the 20B path: update_kv_cache_kernel, attention.hpp:756-778,
+ * and ..._full_bf16kv_okay, attention_mfma.hpp:1679-1900) kb/vb are the
+ * whole caches, bf16 rows [B][cap][kv_dim] at the same rows as the int8
+ * codes, and kq/vq/ks/vs/keep are not used.
  *
  * Build: oracle/Makefile (-ffp-contract=off: no implicit fused multiply-add).
  */
@@ -112,7 +116,7 @@ void orc_kv_quantize_row(const uint16_t *x, int kv_dim, int8_t *q, uint16_t *sca
 /* --------------------------------------------------------- attention -- */
 
 typedef struct {
-    int n_heads, n_kv_heads, head_dim, cap, layer_idx, window, keep, prefix_rule;
+    int n_heads, n_kv_heads, head_dim, cap, layer_idx, window, keep, prefix_rule, cache_bf16;
 } orc_attn_cfg;
 
 /* The dequantised key or value row of token t (run.cpp reads fp32 caches;
@@ -122,6 +126,12 @@ static void orc_kv_row(const orc_attn_cfg *c, int b, int t, int pos, const int8_
                        const uint16_t *cs, const uint16_t *cb, int kvh, float *out) {
     const int kv_dim = c->n_kv_heads * c->head_dim;
     const int odd = c->layer_idx & 1;
+    if (c->cache_bf16) { /* the 20B path's cache: bf16 rows [B][cap][kv_dim] (attention.hpp:756-778) */
+        const int row = (!odd && c->window > 0) ? t % c->window : t;
+        const uint16_t *r = cb + ((size_t)b * c->cap + row) * kv_dim + (size_t)kvh * c->head_dim;
+        for (int i = 0; i < c->head_dim; ++i) out[i] = orc_bf2f(r[i]);
+        return;
+    }
     int bf16 = 0;
     if (odd && c->keep > 0 && cb)
         bf16 = c->prefix_rule == 0 ? (pos < c->keep) : (t < c->keep);
@@ -235,7 +245,7 @@ static void orc_head_phi(const orc_attn_cfg *c, int b, int h, int pos, int split
  * row already written), one layer.  out: fp32 [B][n_heads][head_dim].
  * Returns 0, or -1 for shapes outside what the restatement handles. */
 int orc_attn_decode(int B, int n_heads, int n_kv_heads, int head_dim, int cap, int layer_idx,
-                    int sliding_window, int keep, int prefix_rule, int phi_splits,
+                    int sliding_window, int keep, int prefix_rule, int phi_splits, int cache_bf16,
                     const uint16_t *q, const int8_t *kq, const int8_t *vq, const uint16_t *ks,
                     const uint16_t *vs, const uint16_t *kb, const uint16_t *vb,
                     const uint16_t *sinks, const int32_t *pos, float *out) {
@@ -243,7 +253,7 @@ int orc_attn_decode(int B, int n_heads, int n_kv_heads, int head_dim, int cap, i
         return -1;
     if (phi_splits > 64 || (phi_splits > 0 && head_dim != 64)) return -1;
     const orc_attn_cfg c = {n_heads, n_kv_heads, head_dim, cap, layer_idx, sliding_window, keep,
-                            prefix_rule};
+                            prefix_rule, cache_bf16};
     for (int b = 0; b < B; ++b) {
         const int odd = layer_idx & 1;
         const int rows = (!odd && sliding_window > 0) ? sliding_window : pos[b] + 1;

@@ -45,7 +45,7 @@ _SIGS = {
     "orc_f2h": (ctypes.c_uint16, [_F]),
     "orc_h2f": (_F, [ctypes.c_uint16]),
     "orc_kv_quantize_row": (None, [_P, _I, _P, _P]),
-    "orc_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+    "orc_attn_decode": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                              _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "orc_rope_table": (_I, [_F, _I, _F, _F, _I, _P, _P]),
     "orc_qkv_bias_rope": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
@@ -287,22 +287,28 @@ def kv_quantize_rows(x):
 
 def attn_decode(q, kq, vq, ks, vs, kb, vb, sinks, pos, *, n_kv_heads: int, layer_idx: int,
                 sliding_window: int, keep: int, prefix_rule: int = 0,
-                phi_splits: int = 0) -> np.ndarray:
+                phi_splits: int = 0, cache_bf16: bool = False) -> np.ndarray:
     """Decode attention over logical caches (attn_oracle.c): q bf16
     [B][n_heads][hd]; kq/vq int8 [B][cap][kv_dim]; ks/vs fp16 bits [B][cap];
     kb/vb bf16 [B][keep][kv_dim] or None; sinks bf16 [n_heads]; pos int32 [B].
-    Returns fp32 [B][n_heads][hd]."""
+    cache_bf16: kb/vb are the whole bf16 caches [B][cap][kv_dim] (kq..vs
+    unused, may be None).  Returns fp32 [B][n_heads][hd]."""
     q = _c(q, np.uint16)
     B, NH, HD = q.shape
+    if cache_bf16:
+        cap = kb.shape[1]
+        kq = vq = np.zeros((1,), np.int8)
+        ks = vs = np.zeros((1,), np.uint16)
+    else:
+        cap = kq.shape[1]
     kq, vq = _c(kq, np.int8), _c(vq, np.int8)
-    cap = kq.shape[1]
     ks, vs = _c(ks, np.uint16), _c(vs, np.uint16)
     kb = None if kb is None else _c(kb, np.uint16)
     vb = None if vb is None else _c(vb, np.uint16)
     sinks, pos = _c(sinks, np.uint16), _c(pos, np.int32)
     out = np.empty((B, NH, HD), np.float32)
     rc = lib().orc_attn_decode(B, NH, n_kv_heads, HD, cap, layer_idx, sliding_window, keep,
-                               prefix_rule, phi_splits, _p(q), _p(kq), _p(vq), _p(ks), _p(vs),
+                               prefix_rule, phi_splits, int(cache_bf16), _p(q), _p(kq), _p(vq), _p(ks), _p(vs),
                                _p(kb), _p(vb), _p(sinks), _p(pos), _p(out))
     if rc != 0:
         raise ValueError("orc_attn_decode: shape outside the restatement")

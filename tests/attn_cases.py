@@ -93,3 +93,23 @@ def oracle_out(c: AttnCase, prefix_rule=0, phi_splits=0):
                               c.vb if c.keep else None, c.sinks, c.pos, n_kv_heads=N_KV,
                               layer_idx=c.layer_idx, sliding_window=c.window, keep=c.keep,
                               prefix_rule=prefix_rule, phi_splits=phi_splits)
+
+
+def bf16_caches(c: AttnCase):
+    """The 20B path's caches (update_kv_cache_kernel, attention.hpp:756-778):
+    the bf16 rows themselves at the same rows as the int8 codes.  Returns
+    (kc, vc) bf16 [B][cap][KV]."""
+    kc = np.zeros((c.B, c.cap, KV), np.uint16)
+    vc = np.zeros((c.B, c.cap, KV), np.uint16)
+    for b in range(c.B):
+        for t in range(int(c.pos[b]) + 1):
+            r = c.row_of(t)
+            kc[b, r], vc[b, r] = c.k_hist[b][t], c.v_hist[b][t]
+    return kc, vc
+
+
+def oracle_out_bf16(c: AttnCase, phi_splits=0):
+    kc, vc = bf16_caches(c)
+    return oracle.attn_decode(c.q, None, None, None, None, kc, vc, c.sinks, c.pos, n_kv_heads=N_KV,
+                              layer_idx=c.layer_idx, sliding_window=c.window, keep=0,
+                              phi_splits=phi_splits, cache_bf16=True)

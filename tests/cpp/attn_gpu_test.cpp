@@ -4,7 +4,8 @@
 // attention_cache_and_decode, then the last step again in two row ranges.
 //
 // usage: attn_gpu_test <in.bin> <out.bin>
-// in.bin : int32 B, L, max_seq, window, keep, rule, T; then per step t < T:
+// in.bin : int32 B, L, max_seq, window, keep, rule, T, kind (GPTOSS_ATTN_CACHE_*);
+//          then per step t < T:
 //          k bf16 [B][512], v bf16 [B][512]; then q bf16 [B][64][64]; sinks
 //          bf16 [L][64].  Positions: t for every sequence at step t.
 // out.bin: bf16 [2][L][B][64][64]: state.tb after each layer's call of the
@@ -30,6 +31,7 @@ typedef struct {
 typedef struct {
     __hip_bfloat16 *q, *k, *v, *tb;
     int *positions;
+    __hip_bfloat16 *key_cache_bf16, *value_cache_bf16;
     int8_t *key_cache, *value_cache;
     __half *key_cache_scales, *value_cache_scales;
     __hip_bfloat16 *key_cache_recent_bf16, *value_cache_recent_bf16;
@@ -68,9 +70,10 @@ int main(int argc, char **argv) {
     }
     FILE *f = fopen(argv[1], "rb");
     if (!f) return 2;
-    int32_t hd[7];
+    int32_t hd[8];
     rd(f, hd, sizeof hd);
     const int B = hd[0], L = hd[1], max_seq = hd[2], window = hd[3], keep = hd[4], rule = hd[5], T = hd[6];
+    const int kind = hd[7];
     const int KV = 512, QD = 64 * 64;
     std::vector<uint16_t> kh((size_t)T * B * KV), vh((size_t)T * B * KV), qh((size_t)B * QD), sh((size_t)L * 64);
     for (int t = 0; t < T; ++t) {
@@ -91,6 +94,8 @@ int main(int argc, char **argv) {
     s.v = dalloc<__hip_bfloat16>((size_t)B * KV);
     s.tb = dalloc<__hip_bfloat16>((size_t)B * QD);
     s.positions = dalloc<int>(B);
+    s.key_cache_bf16 = dalloc<__hip_bfloat16>((size_t)B * cap_all * KV);
+    s.value_cache_bf16 = dalloc<__hip_bfloat16>((size_t)B * cap_all * KV);
     s.key_cache = dalloc<int8_t>((size_t)B * cap_all * KV);
     s.value_cache = dalloc<int8_t>((size_t)B * cap_all * KV);
     s.key_cache_scales = dalloc<__half>((size_t)B * cap_all);
@@ -103,7 +108,7 @@ int main(int argc, char **argv) {
 
     hipStream_t st;
     if (hipStreamCreate(&st) != hipSuccess) return 2;
-    gptoss_attn_shim::attn_gpu_init(&gt, B, max_seq, window, keep, rule);
+    gptoss_attn_shim::attn_gpu_init(&gt, B, max_seq, window, keep, rule, kind);
     std::vector<int> pos(B);
     std::vector<uint16_t> out((size_t)2 * L * B * QD);
     for (int t = 0; t < T; ++t) {
@@ -133,6 +138,6 @@ int main(int argc, char **argv) {
     FILE *o = fopen(argv[2], "wb");
     if (!o || fwrite(out.data(), 2, out.size(), o) != out.size()) return 2;
     fclose(o);
-    printf("attn_gpu_test: B %d L %d T %d ok\n", B, L, T);
+    printf("attn_gpu_test: B %d L %d T %d kind %d ok\n", B, L, T, kind);
     return 0;
 }

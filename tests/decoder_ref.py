@@ -1,5 +1,5 @@
 """The decode step of gpt-oss (forward_batch_gpu, getp-csrc/getp_run.cpp:
-3260-3409, attention_gpu :2201-2481, moe_gpu :2540-2887) composed from the
+3260-3409, attention_gpu_120b :2181-2481, moe_gpu :2540-2887) composed from the
 oracle's restatements, with the KV caches in the reference's logical layout.
 Test infrastructure."""
 from __future__ import annotations

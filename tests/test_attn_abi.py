@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 def shape(**kw):
     d = dict(n_heads=64, n_kv_heads=8, head_dim=64, n_layers=24, sliding_window=128, keep=16,
-             prefix_rule=0)
+             prefix_rule=0, cache_kind=0)
     d.update(kw)
     return ga.Shape(*[d[n] for n, _ in ga.Shape._fields_])
 
@@ -69,7 +69,7 @@ def call_both(s, cache, layer, n=4):
 
 @pytest.mark.parametrize("bad", [dict(n_heads=32), dict(n_kv_heads=4), dict(head_dim=128),
                                  dict(sliding_window=100), dict(keep=10), dict(prefix_rule=2),
-                                 dict(n_layers=0)])
+                                 dict(n_layers=0), dict(cache_kind=2)])
 def test_bad_shapes_rejected(bad):
     c = FakeCache().c
     assert call_both(shape(**bad), c, ga.Layer(0, 128, 0, 0)) == (ga.ERR_INVALID_ARG,) * 2
@@ -89,6 +89,16 @@ def test_bad_shapes_rejected(bad):
 def test_bad_layers_rejected(layer, cache_kw):
     c = FakeCache(**cache_kw).c
     assert call_both(shape(), c, layer) == (ga.ERR_INVALID_ARG,) * 2
+
+
+def test_bf16_cache_needs_no_scales():
+    """A bf16 cache (the 20B path) passes the argument checks without scales
+    or kept rows; an int8 cache does not.  Zero sequences: the calls return
+    right after the checks, nothing is launched."""
+    c = FakeCache(key_scales=None, value_scales=None, key_bf16=None, value_bf16=None).c
+    L = ga.Layer(1, 1024, 128 * 512, 128)
+    assert call_both(shape(cache_kind=1), c, L, n=0) == (ga.OK, ga.OK)
+    assert call_both(shape(cache_kind=0), c, L, n=0) == (ga.ERR_INVALID_ARG,) * 2
 
 
 def test_bad_buffers_rejected():

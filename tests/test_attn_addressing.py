@@ -78,7 +78,7 @@ def bf16r(x):
     return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32)))
 
 
-def decode_mirror(c, S, rule, slabs):
+def decode_mirror(c, S, rule, slabs, bf16cache=False):
     """attn_decode_kernel + attn_combine_kernel for case c with S splits;
     slabs: per sequence, the library-layout key, value, bf16 key and bf16
     value slabs of the layer."""
@@ -91,7 +91,9 @@ def decode_mirror(c, S, rule, slabs):
         nvalid = min(pos + 1, c.window) if ring else pos + 1
         nblk = (nvalid + 15) >> 4
         nb16 = 0
-        if not c.even() and c.keep > 0:
+        if bf16cache:
+            nb16 = nblk                     # every block: the cache's own bf16 rows
+        elif not c.even() and c.keep > 0:
             nb16 = (nblk if pos < c.keep else 0) if rule == 0 else min(nblk, c.keep >> 4)
         ksf = c.ks[b].view(np.float16).astype(np.float32)
         vsf = c.vs[b].view(np.float16).astype(np.float32)
@@ -253,3 +255,24 @@ def test_decode_mirror_matches_oracle(layer, pos, keep, S, rule):
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
     assert rel < 4e-3, rel
 
+
+
+@pytest.mark.parametrize("layer,pos,S", [(0, [0, 17, 200], 1), (0, [127, 5], 3), (1, [9, 40, 70], 2),
+                                         (3, [130], 4)])
+def test_decode_mirror_bf16_cache(layer, pos, S):
+    """The bf16 cache (the reference's 20B path): every block through the
+    bf16 path from the cache's layer slab, against the oracle's bf16 mode."""
+    from attn_cases import bf16_caches, oracle_out_bf16
+    c = make_case(51 + layer, layer_idx=layer, pos=pos, keep=16,
+                  cap=None if layer % 2 == 0 else 16 * ((max(pos) + 16) // 16))
+    kc, vc = bf16_caches(c)
+    sk, sv = [], []
+    for b in range(c.B):
+        k, v = from_logical(kc[b], vc[b])
+        sk.append(k)
+        sv.append(v)
+    got = decode_mirror(c, S, 0, ([None] * c.B, [None] * c.B, sk, sv), bf16cache=True)
+    want = oracle_out_bf16(c)
+    err = np.abs(got - want)
+    assert err.max() <= 2e-2 * max(1.0, np.abs(want).max()), err.max()
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 4e-3

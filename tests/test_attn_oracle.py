@@ -209,3 +209,26 @@ def test_phi_semantics_brute_force():
         np.testing.assert_allclose(got[h], want, rtol=2e-4, atol=2e-5)
     assert dropped_any                      # the case exercises the rule
     assert np.abs(got - exact).max() > 0    # and it differs from run.cpp's math
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_bf16_cache_matches_float64_textbook(case):
+    """The 20B path's bf16 cache: the textbook over the history's own bf16
+    rows (no quantisation), with the window on even layers."""
+    from attn_cases import oracle_out_bf16
+    c = make_case(200 + case, **CASES[case])
+    got = oracle_out_bf16(c)
+    want = np.zeros((c.B, N_HEADS, HD))
+    for b in range(c.B):
+        pos = int(c.pos[b])
+        t0 = max(0, pos - c.window + 1) if (c.even() and c.window) else 0
+        K = bf16_to_f32(c.k_hist[b][t0:pos + 1]).astype(np.float64)
+        V = bf16_to_f32(c.v_hist[b][t0:pos + 1]).astype(np.float64)
+        q = bf16_to_f32(c.q[b]).astype(np.float64)
+        for h in range(N_HEADS):
+            g = h // 8
+            s = np.append(K[:, g * HD:(g + 1) * HD] @ q[h] / 8.0, float(bf16_to_f32(c.sinks[h:h + 1])[0]))
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            want[b, h] = p[:-1] @ V[:, g * HD:(g + 1) * HD]
+    assert np.abs(got - want).max() <= 2e-6 * max(1.0, np.abs(want).max())

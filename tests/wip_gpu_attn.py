@@ -29,13 +29,13 @@ def _dev(a, dtype=torch.int16):
                                                          np.int32)).to("cuda:0")
 
 
-def replay(c, rule):
+def replay(c, rule, cache_kind=ga.CACHE_INT8):
     """Write the case's token history into a fresh KvCache one decode step at
     a time (sequences already at their position are skipped, pos = -1)."""
     maxpos = int(c.pos.max())
     max_ctx = c.cap if not c.even() else 16 * ((maxpos + 16) // 16)
     kc = ga.KvCache(c.B, c.layer_idx + 1, max_ctx, sliding_window=c.window, keep=c.keep,
-                    prefix_rule=rule)
+                    prefix_rule=rule, cache_kind=cache_kind)
     for t in range(maxpos + 1):
         pos = np.where(c.pos >= t, t, -1).astype(np.int32)
         k = np.zeros((c.B, KV), np.uint16)
@@ -148,12 +148,15 @@ def test_small_batch_split_matches_unsplit():
     parity.assert_close(f32_to_bf16(b), want, "attn split 1024")
 
 
-def test_cpp_attention_shim(tmp_path):
+@pytest.mark.parametrize("kind", [0, 1])
+def test_cpp_attention_shim(tmp_path, kind):
     """The attention shim from C++ (tests/cpp/attn_gpu_test.cpp over
     gpt-oss_amd/csrc/attn_gpu_shim.hpp, the reference's state member names):
     40 steps of 2 layers (a 32-row ring, 16 bf16-kept tokens, the mixed
-    rule), the last step's outputs against the oracle, and the same step run
-    as two row ranges (row_offset) bit-identical to the whole batch."""
+    rule), with the int8 cache (attention_gpu_120b) and the bf16 cache
+    (attention_gpu), the last step's outputs against the oracle, and the
+    same step run as two row ranges (row_offset) bit-identical to the whole
+    batch."""
     import os
     import subprocess
     from attn_cases import AttnCase, write_caches
@@ -169,7 +172,7 @@ def test_cpp_attention_shim(tmp_path):
     sinks = f32_to_bf16(rng.standard_normal((L, 64)).astype(np.float32))
     inp = tmp_path / "in.bin"
     with open(inp, "wb") as f:
-        f.write(np.array([B, L, max_seq, window, keep, rule, T], np.int32).tobytes())
+        f.write(np.array([B, L, max_seq, window, keep, rule, T, kind], np.int32).tobytes())
         for t in range(T):
             f.write(kh[t].tobytes())
             f.write(vh[t].tobytes())
@@ -185,6 +188,33 @@ def test_cpp_attention_shim(tmp_path):
         c = AttnCase(l, window, keep, window if l % 2 == 0 else max_seq, np.full(B, T - 1, np.int32), q,
                      [kh[:, b] for b in range(B)], [vh[:, b] for b in range(B)], sinks[l])
         write_caches(c)
-        want = f32_to_bf16(oracle_out(c, prefix_rule=rule))
-        m = parity.assert_close(out[0, l], want, f"attention shim from C++, layer {l}")
+        if kind == 1:  # attention_gpu's bf16 cache
+            from attn_cases import oracle_out_bf16
+            want = f32_to_bf16(oracle_out_bf16(c))
+        else:
+            want = f32_to_bf16(oracle_out(c, prefix_rule=rule))
+        m = parity.assert_close(out[0, l], want, f"attention shim from C++, layer {l}, cache kind {kind}")
+        assert m["rel_l2"] <= TIGHT_REL_L2, m
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_bf16_cache(name):
+    """The reference's 20B path: bf16 rows in the cache (no quantisation),
+    written bit for bit, and the decode against the oracle's bf16 mode."""
+    from attn_cases import bf16_caches, oracle_out_bf16
+    kw = dict(CASES[name])
+    if kw["layer_idx"] % 2:
+        kw["cap"] = 16 * ((max(kw["pos"]) + 16) // 16)
+    c = make_case(700 + sorted(CASES).index(name), **kw)
+    kc = replay(c, 0, cache_kind=ga.CACHE_BF16)
+    kslab, vslab, _, _, _, _ = kc.layer_slabs(c.layer_idx)
+    ref_k, ref_v = bf16_caches(c)
+    for b in range(c.B):
+        lk, lv = to_logical(kslab[b], vslab[b], c.cap)
+        assert np.array_equal(lk, ref_k[b]) and np.array_equal(lv, ref_v[b]), f"rows of sequence {b}"
+    want = f32_to_bf16(oracle_out_bf16(c))
+    q, sinks, pos = _dev(c.q), _dev(c.sinks), _dev(c.pos, torch.int32)
+    for split in (False, True):
+        got = kc.decode(c.layer_idx, q, sinks, pos, split=split).view(torch.int16).cpu().numpy().view(np.uint16)
+        m = parity.assert_close(got, want, f"attn bf16 cache {name} split {split}")
         assert m["rel_l2"] <= TIGHT_REL_L2, m
