@@ -2483,7 +2483,11 @@ struct SCursor {
 };
 
 // One stage (NKS k steps of 32) of consumer c: weight unit c of the item
-// against MT 16-row groups of the tile.
+// against MT 16-row groups of the tile.  The weights are the MFMA's A operand
+// and the activation rows its B operand, so acc[m][t] is the transposed
+// product: lane n + 16 g holds weight rows 4 g .. 4 g + 3 of column tile t
+// against tile row 16 m + n (the epilogue then owns 4 consecutive output
+// columns of one row per lane).
 template <int MT, int NKS>
 __device__ __forceinline__ void s_compute(const SWSlot &ws, const SASlot &as, int c,
                                           f32x4 (&acc)[4][2]) {
@@ -2510,12 +2514,18 @@ __device__ __forceinline__ void s_compute(const SWSlot &ws, const SASlot &as, in
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(arow + m * 4096 + uo));
-            acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[0], acc[m][0], 0, 0, 0);
-            acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[1], acc[m][1], 0, 0, 0);
+            acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[0], a, acc[m][0], 0, 0, 0);
+            acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[1], a, acc[m][1], 0, 0, 0);
         }
     }
 }
 
+// Epilogue of consumer c (acc as s_compute leaves it: lane n + 16 g, tile
+// row 16 m + n, weight rows 4 g + v of tiles 0 and 1).  MLP1: tile 0 holds
+// the gate rows and tile 1 the up rows of output columns 16 (f + c) .. + 15,
+// so the lane's 4 outputs 16 (f + c) + 4 g + v are adjacent: one 8-byte
+// store per row.  MLP2: tile t holds output columns 32 (f + c) + 16 t + 4 g
+// + v: two 8-byte stores per row into its token-order slot.
 template <int MT, bool kMlp1>
 __device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlot &ws, const Tile &tl,
                                            int f, int c, const f32x4 (&acc)[4][2]) {
@@ -2523,39 +2533,48 @@ __device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlot &ws, 
     const int N = a.N;
     if (kMlp1) {
         const int D = N / 2;
-        const int jc = 16 * (f + c) + n;  // output column: gate row 2 jc, up row 2 jc + 1
-        const uint32_t gu = reinterpret_cast<const uint32_t *>(ws.bias)[16 * c + n];
-        const float bg = __uint_as_float(gu << 16);
-        const float bu = __uint_as_float(gu & 0xffff0000u);
+        const int j0 = 16 * (f + c) + 4 * g;  // the lane's first output column: gate row 2 j0, up 2 j0 + 1
+        // (gate, up) bias pairs of columns j0 .. j0 + 3, bf16 each
+        const u32x4 gu = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint32_t *>(ws.bias) + 16 * c + 4 * g);
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < MT; ++m) {
+            const int r = 16 * m + n;
+            if (r < tl.rows) {
+                uint32_t o[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = 16 * m + 4 * g + v;
-                if (r < tl.rows) {
-                    float gt = bf16_round(acc[m][0][v] + bg);
-                    float up = bf16_round(acc[m][1][v] + bu);
+                for (int v = 0; v < 4; ++v) {
+                    float gt = bf16_round(acc[m][0][v] + __uint_as_float(gu[v] << 16));
+                    float up = bf16_round(acc[m][1][v] + __uint_as_float(gu[v] & 0xffff0000u));
                     gt = fminf(fmaxf(gt, -a.limit), a.limit);
                     up = fminf(fmaxf(up, -a.limit), a.limit);
                     const float sig = 1.0f / (1.0f + __expf(-a.alpha * gt));
                     gt = gt * sig;
-                    a.out_act[(size_t)(tl.row0 + r) * D + jc] = f2bf(__builtin_fmaf(gt, up, gt));
+                    o[v] = f2bf(__builtin_fmaf(gt, up, gt));
                 }
+                *reinterpret_cast<uint2 *>(a.out_act + (size_t)(tl.row0 + r) * D + j0) =
+                    make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
             }
+        }
     } else {
-        const int h = 32 * (f + c) + n;
-        const float b0 = bf2f(ws.bias[32 * c + n]), b1 = bf2f(ws.bias[32 * c + 16 + n]);
+        const int h = 32 * (f + c) + 4 * g;
+        const uint2 b0 = *reinterpret_cast<const uint2 *>(ws.bias + 32 * c + 4 * g);
+        const uint2 b1 = *reinterpret_cast<const uint2 *>(ws.bias + 32 * c + 16 + 4 * g);
+        const uint32_t bw[2][4] = {{b0.x & 0xffffu, b0.x >> 16, b0.y & 0xffffu, b0.y >> 16},
+                                   {b1.x & 0xffffu, b1.x >> 16, b1.y & 0xffffu, b1.y >> 16}};
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < MT; ++m) {
+            const int r = 16 * m + n;
+            if (r < tl.rows) {
+                uint16_t *dst = a.out_slots + (size_t)ws.slot[r] * N + h;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = 16 * m + 4 * g + v;
-                if (r < tl.rows) {
-                    uint16_t *dst = a.out_slots + (size_t)ws.slot[r] * N + h;
-                    dst[0] = f2bf(acc[m][0][v] + b0);
-                    dst[16] = f2bf(acc[m][1][v] + b1);
+                for (int t = 0; t < 2; ++t) {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) o[v] = f2bf(acc[m][t][v] + __uint_as_float(bw[t][v] << 16));
+                    *reinterpret_cast<uint2 *>(dst + 16 * t) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
                 }
             }
+        }
     }
 }
 

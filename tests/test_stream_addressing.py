@@ -188,3 +188,88 @@ def test_lds_layout_fits():
     wslot = 16 * 1024 + 1024 + 1024 + 256
     aslot = 64 * 256
     assert 5 * wslot + 4 * aslot <= 160 * 1024
+
+
+def mfma_transposed_acc(w_tiles, x_rows, MT):
+    """s_compute's accumulators for one consumer: the weights are the A
+    operand of v_mfma_f32_16x16x32_bf16 and the activation rows its B
+    operand, so D_t = W_t . X^T (16 weight rows x 16 tile rows per group m),
+    and lane n + 16 g holds D_t rows 4 g .. 4 g + 3 of column n.  Returns
+    acc[lane][m][t][v]."""
+    acc = np.zeros((64, 4, 2, 4), np.float32)
+    for m in range(MT):
+        xm = np.zeros((16, x_rows.shape[1]), np.float32)
+        blk = x_rows[16 * m:16 * m + 16]
+        xm[:len(blk)] = blk
+        for t in range(2):
+            D = w_tiles[t] @ xm.T                  # [16 weight rows][16 tile rows]
+            for lane in range(64):
+                n, g = lane & 15, lane >> 4
+                acc[lane, m, t] = D[4 * g:4 * g + 4, n]
+    return acc
+
+
+def swiglu(gt, up, alpha=1.702, limit=7.0):
+    gt = np.clip(gt, -limit, limit)
+    up = np.clip(up, -limit, limit)
+    gt = gt / (1 + np.exp(-alpha * gt))
+    return gt * up + gt
+
+
+@pytest.mark.parametrize("mlp1", [True, False])
+@pytest.mark.parametrize("rows", [1, 5, 16, 17, 37, 64])
+def test_epilogue_lane_columns(mlp1, rows):
+    """s_epilogue on the transposed accumulators: every output element of
+    the tile's rows is written once, by the lane and 8-byte store the kernel
+    names, with the right bias; rows past tl.rows are not written.  The
+    weights are placed by the packed layout's row order (MLP1: tile 0 the
+    gate rows, tile 1 the up rows of 16 output columns)."""
+    rng = np.random.default_rng(rows + 100 * mlp1)
+    N, K, f, cnt, row0 = 256, 64, 2, 3, 5
+    W = rng.standard_normal((N, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    X = rng.standard_normal((rows, K)).astype(np.float32)
+    MT = -(-rows // 16)
+    D = N // 2 if mlp1 else N
+    n_out_rows = row0 + rows + 3
+    out = np.full((n_out_rows, D), np.nan, np.float32)
+    writes = np.zeros((n_out_rows, D), np.int64)
+    slot = rng.permutation(n_out_rows)[:64]          # MLP2: token-order slot of tile row r
+    pr = np.arange(N)
+    src = ((pr & ~31) + 2 * (pr & 15) + ((pr >> 4) & 1)) if mlp1 else pr  # packed row -> weight row
+    wb = bias[32 * f:32 * (f + cnt)]                   # the item's biases in the ring slot (weight-row order)
+    for c in range(cnt):
+        u = f + c
+        tiles = [W[src[32 * u + 16 * t:32 * u + 16 * t + 16]] for t in range(2)]
+        acc = mfma_transposed_acc(tiles, X, MT)
+        for lane in range(64):
+            n, g = lane & 15, lane >> 4
+            for m in range(MT):
+                r = 16 * m + n
+                if r >= rows:
+                    continue
+                if mlp1:
+                    j0 = 16 * (f + c) + 4 * g
+                    assert ((row0 + r) * D + j0) % 4 == 0    # 8-byte aligned bf16 store
+                    for v in range(4):
+                        bg, bu = wb[2 * (16 * c + 4 * g + v)], wb[2 * (16 * c + 4 * g + v) + 1]
+                        out[row0 + r, j0 + v] = swiglu(acc[lane, m, 0, v] + bg, acc[lane, m, 1, v] + bu)
+                        writes[row0 + r, j0 + v] += 1
+                else:
+                    h = 32 * (f + c) + 4 * g
+                    for t in range(2):
+                        assert (slot[r] * N + h + 16 * t) % 4 == 0
+                        for v in range(4):
+                            out[slot[r], h + 16 * t + v] = acc[lane, m, t, v] + wb[32 * c + 16 * t + 4 * g + v]
+                            writes[slot[r], h + 16 * t + v] += 1
+    cols = slice(16 * f, 16 * (f + cnt)) if mlp1 else slice(32 * f, 32 * (f + cnt))
+    Y = X @ W.T + bias                                  # [rows][N], weight-row order
+    if mlp1:
+        want = swiglu(Y[:, 0::2], Y[:, 1::2])[:, cols]
+        got, wr = out[row0:row0 + rows, cols], writes[row0:row0 + rows, cols]
+    else:
+        want = Y[:, cols]
+        got, wr = out[slot[:rows], cols], writes[slot[:rows], cols]
+    assert (wr == 1).all()
+    assert writes.sum() == wr.size                      # nothing else written
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
