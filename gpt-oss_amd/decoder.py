@@ -48,6 +48,7 @@ class DecoderConfig:
     rope_theta: float = 150000.0
     rope_scaling: float = 32.0
     initial_context_length: float = 4096.0
+    cache_kind: int = ga.CACHE_INT8  # CACHE_BF16: the 20B reference path's bf16 KV cache
 
 
 def rope_table(cfg: DecoderConfig):
@@ -81,7 +82,8 @@ class Decoder:
         self.moe = moe
         self.lib = ga.load_library()
         self.kv = ga.KvCache(n_seqs, cfg.n_layers, cfg.max_ctx, sliding_window=cfg.sliding_window,
-                             keep=cfg.keep, prefix_rule=cfg.prefix_rule, device=device)
+                             keep=cfg.keep, prefix_rule=cfg.prefix_rule, device=device,
+                             cache_kind=cfg.cache_kind)
         c, s = rope_table(cfg)
         self.cos = torch.from_numpy(c).to(self.dev)
         self.sin = torch.from_numpy(s).to(self.dev)
@@ -232,3 +234,61 @@ def random_on_device(cfg: DecoderConfig, n_seqs: int, seed: int = 0xC4, device="
         lay.drop_unpacked()
         moe.append(lay)
     return Decoder(cfg, n_seqs, w, moe, device)
+
+
+def config_from_json(cfg: dict, max_ctx: int = 1024, keep: int = 128, prefix_rule: int = ga.PREFIX_MIXED,
+                     cache_kind: int = ga.CACHE_INT8) -> DecoderConfig:
+    """DecoderConfig from the checkpoint's config.json (the fields of
+    export_model_bin.py:33-39 that the decode step uses).  The attention
+    shape is fixed by the kernels: 64 query heads, 8 KV heads, head_dim 64."""
+    if (cfg.get("num_attention_heads"), cfg.get("num_key_value_heads"), cfg.get("head_dim")) != \
+            (N_HEADS, N_KV, HD):
+        raise ValueError("attention shape {}/{}/{} is not the supported {}/{}/{}".format(
+            cfg.get("num_attention_heads"), cfg.get("num_key_value_heads"), cfg.get("head_dim"),
+            N_HEADS, N_KV, HD))
+    return DecoderConfig(hidden=int(cfg["hidden_size"]), intermediate=int(cfg["intermediate_size"]),
+                         n_experts=int(cfg["num_experts"]), top_k=int(cfg["experts_per_token"]),
+                         n_layers=int(cfg["num_hidden_layers"]), vocab=int(cfg["vocab_size"]),
+                         max_ctx=max_ctx, sliding_window=int(cfg.get("sliding_window", 0)), keep=keep,
+                         prefix_rule=prefix_rule, rope_theta=float(cfg["rope_theta"]),
+                         rope_scaling=float(cfg["rope_scaling_factor"]),
+                         initial_context_length=float(cfg["initial_context_length"]), cache_kind=cache_kind)
+
+
+def checkpoint_host_weights(ckpt, cfg: DecoderConfig) -> dict:
+    """The decoder's non-MoE weights from a checkpoint.Checkpoint, as numpy
+    bf16 bits in the layout of make_host_weights (emb, out, rms_out and the
+    per-layer lists); the MoE layers are read per layer by
+    gptoss_moe.MoeLayer.from_checkpoint."""
+    H = cfg.hidden
+    w = {"emb": ckpt.bf16("embedding.weight", (cfg.vocab, H)),
+         "out": ckpt.bf16("unembedding.weight", (cfg.vocab, H)), "rms_out": ckpt.bf16("norm.scale", (H,)),
+         "rms_attn": [], "w_qkv": [], "b_qkv": [], "w_o": [], "b_o": [], "sinks": [], "rms_ffn": []}
+    for l in range(cfg.n_layers):
+        a = ckpt.attention_layer(l, H, N_HEADS, N_KV, HD)
+        for k, v in a.items():
+            w[k].append(v)
+        w["rms_ffn"].append(ckpt.bf16(f"block.{l}.mlp.norm.scale", (H,)))
+    return w
+
+
+def from_checkpoint(path: str, n_seqs: int, max_ctx: int = 1024, keep: int = 128,
+                    prefix_rule: int = ga.PREFIX_MIXED, cache_kind: int = ga.CACHE_INT8,
+                    device="cuda") -> Decoder:
+    """A Decoder over the original gpt-oss checkpoint in directory `path`
+    (config.json + *.safetensors): MoE weights packed byte for byte from the
+    MXFP4 blocks (the unpacked copies freed), everything else in bf16."""
+    import torch
+    import checkpoint as ck
+    raw = ck.read_config(path)
+    cfg = config_from_json(raw, max_ctx, keep, prefix_rule, cache_kind)
+    ckpt = ck.Checkpoint(path)
+    if ckpt.n_layers() != cfg.n_layers:
+        raise ValueError(f"checkpoint holds {ckpt.n_layers()} layers, config.json says {cfg.n_layers}")
+    dev = torch.device(device)
+    up = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    hw = checkpoint_host_weights(ckpt, cfg)
+    dw = {k: ([up(a) for a in v] if isinstance(v, list) else up(v)) for k, v in hw.items()}
+    moe = [gm.MoeLayer.from_checkpoint((ckpt, raw), l, n_seqs, device, drop_unpacked=True)
+           for l in range(cfg.n_layers)]
+    return Decoder(cfg, n_seqs, dw, moe, device)

@@ -272,6 +272,49 @@ class MoeLayer:
         return cls(shape, w, max_tokens or c.tokens, device, pack=pack, pack_fp4=pack_fp4)
 
     @classmethod
+    def from_arrays(cls, arrays: dict, top_k: int, max_tokens: int, limit: float = 7.0,
+                    device="cuda", pack: bool = True) -> "MoeLayer":
+        """Upload numpy weights in include/gptoss_moe.h's layouts (the dict of
+        checkpoint.Checkpoint.moe_layer: router_w, router_b, w1, w1_scales,
+        b1, w2, w2_scales, b2 as arrays, hidden / intermediate / n_experts as
+        ints, optional rms_ffn_w kept in tensors["rms_ffn_w"])."""
+        import torch
+        dev = torch.device(device)
+
+        def up(a):
+            a = np.ascontiguousarray(a)
+            if a.dtype == np.uint16:
+                a = a.view(np.int16)
+            return torch.from_numpy(a).to(dev)
+
+        names = ("router_w", "router_b", "w1", "w1_scales", "b1", "w2", "w2_scales", "b2")
+        w = {n: up(arrays[n]) for n in names}
+        shape = make_shape(arrays["hidden"], arrays["intermediate"], arrays["n_experts"], top_k, limit)
+        layer_obj = cls(shape, w, max_tokens, device, pack=pack)
+        if "rms_ffn_w" in arrays:
+            layer_obj.tensors["rms_ffn_w"] = up(arrays["rms_ffn_w"])
+        return layer_obj
+
+    @classmethod
+    def from_checkpoint(cls, path, layer: int, max_tokens: int, device="cuda", pack: bool = True,
+                        drop_unpacked: bool = False) -> "MoeLayer":
+        """Layer `layer` of the original gpt-oss checkpoint (a .safetensors
+        file or directory with config.json, or a checkpoint.Checkpoint plus
+        its config as a (ckpt, config) pair): the MXFP4 blocks and scales byte
+        for byte, the rest in bf16.  top_k and the SwiGLU limit come from the
+        config (experts_per_token, swiglu_limit)."""
+        import checkpoint as ck
+        if isinstance(path, tuple):
+            ckpt, cfg = path
+        else:
+            ckpt, cfg = ck.Checkpoint(path), ck.read_config(os.path.dirname(path) if os.path.isfile(path) else path)
+        lay = cls.from_arrays(ckpt.moe_layer(layer), int(cfg["experts_per_token"]), max_tokens,
+                              float(cfg.get("swiglu_limit", 7.0)), device, pack)
+        if drop_unpacked:
+            lay.drop_unpacked()
+        return lay
+
+    @classmethod
     def from_bin(cls, path: str, layer: int, max_tokens: int, device="cuda", pack: bool = True,
                  stage_bytes: int = 64 << 20) -> "MoeLayer":
         """Layer `layer` of the reference's fp32 checkpoint (gptoss_moe_load_bin_layer):
