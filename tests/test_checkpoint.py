@@ -100,7 +100,7 @@ def test_decoder_config_and_weights(small):
     path, t = small
     cfg = dec.config_from_json(ck.read_config(path), max_ctx=64, keep=16)
     assert (cfg.hidden, cfg.intermediate, cfg.n_experts, cfg.top_k, cfg.n_layers, cfg.vocab) == \
-        (128, 64, 4, 2, 2, 96)
+        (128, 128, 4, 2, 2, 96)
     assert (cfg.sliding_window, cfg.rope_theta, cfg.rope_scaling, cfg.initial_context_length) == \
         (32, 150000.0, 32.0, 4096.0)
     w = dec.checkpoint_host_weights(ck.Checkpoint(path), cfg)
