@@ -204,8 +204,7 @@ __global__ __launch_bounds__(64) void kv_update_kernel(KvArgs a) {
         a.vs[so] = f2h(safe_v / 127.f);
     }
     if (a.odd && pos < a.keep) {  // the bf16 copy (attention.hpp:630-652)
-        const size_t slab = a.bf16cache ? (size_t)b * a.bks + a.lko  // the bf16 cache's layer
-                                        : ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
+        const size_t slab = ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
         const size_t bt = slab + (size_t)((pos >> 4) * kKvHeads + kvh) * kTile;
         *(u32x4 *)(a.kb + bt + (pos & 15) * 64 + d0) = kr;
 #pragma unroll
@@ -468,7 +467,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3, 8))) void
     // bf16 rows first (odd layers' kept tokens), then the int8 rows
     const int e16 = min(blk1, nb16);
     if (blk0 < e16) {
-        const size_t slab = ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
+        // the kept-token slab of (sequence, layer), or with the bf16 cache the
+        // layer's rows of the sequence (the same base kv_update_kernel writes)
+        const size_t slab = a.bf16cache ? (size_t)b * a.bks + a.lko
+                                        : ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
         for (int blk = blk0; blk < e16; blk += 2) {
             const int nb = min(2, e16 - blk);
             BlkBf A, B;

@@ -78,14 +78,25 @@ def bf16r(x):
     return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32)))
 
 
-def decode_mirror(c, S, rule, slabs, bf16cache=False):
-    """attn_decode_kernel + attn_combine_kernel for case c with S splits;
-    slabs: per sequence, the library-layout key, value, bf16 key and bf16
-    value slabs of the layer."""
+def decode_mirror(c, S, rule, bufs, bf16cache=False):
+    """attn_decode_kernel + attn_combine_kernel for case c with S splits over
+    whole cache buffers (library_buffers); each sequence's slabs are found
+    with the kernel's base formulas."""
     B = c.B
     out = np.zeros((B, N_HEADS, HD), np.float32)
     for b in range(B):
-        slab_k, slab_v, kb_slab, vb_slab = (x[b] for x in slabs)
+        kv0, s0 = b * bufs["bks"] + bufs["lko"], b * bufs["bss"] + bufs["lso"]
+        n = c.cap * KV
+        if bf16cache:   # the cache's own rows: codes buffers hold bf16, slab b bks + lko
+            slab_k = slab_v = None
+            kb_slab, vb_slab = bufs["kc"][kv0:kv0 + n], bufs["vc"][kv0:kv0 + n]
+            ksf = vsf = None
+        else:
+            slab_k, slab_v = bufs["kc"][kv0:kv0 + n], bufs["vc"][kv0:kv0 + n]
+            kp = (b * bufs["n_layers"] + c.layer_idx) * c.keep * KV   # kept-token slab
+            kb_slab, vb_slab = bufs["kb"][kp:kp + c.keep * KV], bufs["vb"][kp:kp + c.keep * KV]
+            ksf = bufs["ks"][s0:s0 + c.cap].view(np.float16).astype(np.float32)
+            vsf = bufs["vs"][s0:s0 + c.cap].view(np.float16).astype(np.float32)
         pos = int(c.pos[b])
         ring = c.even() and c.window > 0
         nvalid = min(pos + 1, c.window) if ring else pos + 1
@@ -95,8 +106,6 @@ def decode_mirror(c, S, rule, slabs, bf16cache=False):
             nb16 = nblk                     # every block: the cache's own bf16 rows
         elif not c.even() and c.keep > 0:
             nb16 = (nblk if pos < c.keep else 0) if rule == 0 else min(nblk, c.keep >> 4)
-        ksf = c.ks[b].view(np.float16).astype(np.float32)
-        vsf = c.vs[b].view(np.float16).astype(np.float32)
         for kvh in range(N_KV):
             parts = []
             for s in range(S):
@@ -220,17 +229,41 @@ def decode_mirror(c, S, rule, slabs, bf16cache=False):
     return out
 
 
-def library_slabs(c):
-    """The caches in the library's layout (one layer slab per sequence)."""
-    sk, sv, kbs, vbs = [], [], [], []
-    for b in range(c.B):
-        k, v = from_logical(c.kq[b], c.vq[b])
-        sk.append(k)
-        sv.append(v)
-        kb, vb = from_logical(c.kb[b], c.vb[b]) if c.keep else (np.zeros(0, np.uint16),) * 2
-        kbs.append(kb)
-        vbs.append(vb)
-    return sk, sv, kbs, vbs
+def library_buffers(c, kc=None, vc=None, lead=48, tail=32, seed=0):
+    """Whole cache buffers as the library holds them: per sequence `lead`
+    rows of other layers, this layer's cap rows in the library's layout, then
+    `tail` rows, all other memory random (a wrong base reads garbage); the
+    kept-token buffer [B][n_layers][keep][KV] with this layer at its index.
+    kc, vc: bf16 logical caches [B][cap][KV] for the bf16 cache kind."""
+    rng = np.random.default_rng(seed)
+    B, cap = c.B, c.cap
+    rows = lead + cap + tail
+    n_layers = c.layer_idx + 2
+    bf = kc is not None
+    dt = np.uint16 if bf else np.int8
+    big = lambda n: rng.integers(-100, 100, n).astype(dt) if not bf else \
+        f32_to_bf16(rng.standard_normal(n).astype(np.float32) * 50)
+    out = {"bks": rows * KV, "lko": lead * KV, "bss": rows, "lso": lead, "n_layers": n_layers,
+           "kc": big(B * rows * KV), "vc": big(B * rows * KV),
+           # garbage fp16 scales (1 .. 4) outside the layer's rows
+           "ks": rng.integers(0x3C00, 0x4400, B * rows).astype(np.uint16),
+           "vs": rng.integers(0x3C00, 0x4400, B * rows).astype(np.uint16)}
+    keep = max(c.keep, 1)
+    out["kb"] = f32_to_bf16(rng.standard_normal(B * n_layers * keep * KV).astype(np.float32) * 50)
+    out["vb"] = f32_to_bf16(rng.standard_normal(B * n_layers * keep * KV).astype(np.float32) * 50)
+    for b in range(B):
+        k, v = from_logical(kc[b], vc[b]) if bf else from_logical(c.kq[b], c.vq[b])
+        o = b * out["bks"] + out["lko"]
+        out["kc"][o:o + cap * KV], out["vc"][o:o + cap * KV] = k, v
+        if bf:
+            continue
+        so = b * out["bss"] + out["lso"]
+        out["ks"][so:so + cap], out["vs"][so:so + cap] = c.ks[b], c.vs[b]
+        if c.keep:
+            kb, vb = from_logical(c.kb[b], c.vb[b])
+            kp = (b * n_layers + c.layer_idx) * c.keep * KV
+            out["kb"][kp:kp + c.keep * KV], out["vb"][kp:kp + c.keep * KV] = kb, vb
+    return out
 
 
 @pytest.mark.parametrize("layer,pos,keep,S,rule", [
@@ -243,12 +276,13 @@ def library_slabs(c):
 def test_decode_mirror_matches_oracle(layer, pos, keep, S, rule):
     c = make_case(31 + layer, layer_idx=layer, pos=pos, keep=keep,
                   cap=None if layer % 2 == 0 else 16 * ((max(pos) + 16) // 16))
-    slabs = library_slabs(c)
+    bufs = library_buffers(c, seed=layer)
     # round trip of the layout helpers
     for b in range(c.B):
-        lk, lv = to_logical(slabs[0][b], slabs[1][b], c.cap)
+        o = b * bufs["bks"] + bufs["lko"]
+        lk, lv = to_logical(bufs["kc"][o:o + c.cap * KV], bufs["vc"][o:o + c.cap * KV], c.cap)
         assert np.array_equal(lk, c.kq[b]) and np.array_equal(lv, c.vq[b])
-    got = decode_mirror(c, S, rule, slabs)
+    got = decode_mirror(c, S, rule, bufs)
     want = oracle_out(c, prefix_rule=rule)
     err = np.abs(got - want)
     assert err.max() <= 2e-2 * max(1.0, np.abs(want).max()), err.max()
@@ -266,12 +300,7 @@ def test_decode_mirror_bf16_cache(layer, pos, S):
     c = make_case(51 + layer, layer_idx=layer, pos=pos, keep=16,
                   cap=None if layer % 2 == 0 else 16 * ((max(pos) + 16) // 16))
     kc, vc = bf16_caches(c)
-    sk, sv = [], []
-    for b in range(c.B):
-        k, v = from_logical(kc[b], vc[b])
-        sk.append(k)
-        sv.append(v)
-    got = decode_mirror(c, S, 0, ([None] * c.B, [None] * c.B, sk, sv), bf16cache=True)
+    got = decode_mirror(c, S, 0, library_buffers(c, kc, vc, seed=layer), bf16cache=True)
     want = oracle_out_bf16(c)
     err = np.abs(got - want)
     assert err.max() <= 2e-2 * max(1.0, np.abs(want).max()), err.max()
