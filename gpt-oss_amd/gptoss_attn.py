@@ -129,13 +129,16 @@ class KvCache:
         code_dtype = torch.int16 if cache_kind == CACHE_BF16 else torch.int8
         self.key_codes = torch.zeros(n_seqs * rows * KV_DIM, dtype=code_dtype, device=device)
         self.value_codes = torch.zeros_like(self.key_codes)
-        self.key_scales = torch.zeros(n_seqs * rows, dtype=torch.int16, device=device)
+        n_scales = 1 if cache_kind == CACHE_BF16 else n_seqs * rows  # the bf16 kind has none
+        self.key_scales = torch.zeros(n_scales, dtype=torch.int16, device=device)
         self.value_scales = torch.zeros_like(self.key_scales)
         nb = max(1, n_seqs * n_layers * keep * KV_DIM)
         self.key_bf16 = torch.zeros(nb, dtype=torch.int16, device=device)
         self.value_bf16 = torch.zeros_like(self.key_bf16)
+        bf = cache_kind == CACHE_BF16
         self.cache = Cache(self.key_codes.data_ptr(), self.value_codes.data_ptr(),
-                           self.key_scales.data_ptr(), self.value_scales.data_ptr(),
+                           None if bf else self.key_scales.data_ptr(),
+                           None if bf else self.value_scales.data_ptr(),
                            self.key_bf16.data_ptr() if keep else None,
                            self.value_bf16.data_ptr() if keep else None,
                            rows * KV_DIM, rows)
@@ -175,11 +178,15 @@ class KvCache:
     def layer_slabs(self, l: int):
         """This layer's raw slabs per sequence, as CPU numpy arrays: key codes,
         value codes [n][cap * 512] (library tile order), scales [n][cap], and
-        bf16 rows [n][keep * 512] (odd layers)."""
+        bf16 rows [n][keep * 512] (odd layers); with the bf16 cache kind the
+        bf16 rows [n][cap * 512] and four Nones."""
         import numpy as np
         rows, cap, off = self.rows, self.caps[l], self.offsets[l]
         kc = self.key_codes.view(self.n_seqs, rows * KV_DIM)[:, off * KV_DIM:(off + cap) * KV_DIM]
         vc = self.value_codes.view(self.n_seqs, rows * KV_DIM)[:, off * KV_DIM:(off + cap) * KV_DIM]
+        cpu = lambda t: None if t is None else t.cpu().numpy()
+        if self.cache_kind == CACHE_BF16:  # bf16 rows [n][cap * 512], no scales or kept rows
+            return cpu(kc).view(np.uint16), cpu(vc).view(np.uint16), None, None, None, None
         ks = self.key_scales.view(self.n_seqs, rows)[:, off:off + cap]
         vs = self.value_scales.view(self.n_seqs, rows)[:, off:off + cap]
         keep = self.shape.keep
@@ -187,10 +194,6 @@ class KvCache:
             self.n_seqs, self.n_layers, keep * KV_DIM)[:, l] if keep else None
         vb = self.value_bf16[:self.n_seqs * self.n_layers * keep * KV_DIM].view(
             self.n_seqs, self.n_layers, keep * KV_DIM)[:, l] if keep else None
-        cpu = lambda t: None if t is None else t.cpu().numpy()
-        if self.cache_kind == CACHE_BF16:
-            kc, vc = cpu(kc).view(np.uint16), cpu(vc).view(np.uint16)
-            return kc, vc, None, None, None, None
         return (cpu(kc), cpu(vc), cpu(ks).view(np.uint16), cpu(vs).view(np.uint16),
                 None if kb is None else cpu(kb).view(np.uint16),
                 None if vb is None else cpu(vb).view(np.uint16))

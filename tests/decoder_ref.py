@@ -1,6 +1,7 @@
 """The decode step of gpt-oss (forward_batch_gpu, getp-csrc/getp_run.cpp:
 3260-3409, attention_gpu_120b :2181-2481, moe_gpu :2540-2887) composed from the
-oracle's restatements, with the KV caches in the reference's logical layout.
+oracle's restatements, with the KV caches in the reference's logical layout (int8 codes, or the
+20B path's bf16 rows when cfg.cache_kind is 1).
 Test infrastructure."""
 from __future__ import annotations
 
@@ -26,6 +27,10 @@ class OracleDecoder:
         keep = max(cfg.keep, 1)
         self.kb = [np.zeros((B, keep, KV), np.uint16) for _ in self.caps]
         self.vb = [np.zeros((B, keep, KV), np.uint16) for _ in self.caps]
+        # the 20B path's bf16 cache (update_kv_cache_kernel, attention.hpp:756-778)
+        self.bf16_cache = getattr(cfg, "cache_kind", 0) == 1
+        self.kc = [np.zeros((B, c, KV), np.uint16) for c in self.caps]
+        self.vc = [np.zeros((B, c, KV), np.uint16) for c in self.caps]
 
     def kv_update(self, l, k, v, pos):
         """quantize_kv_cache_kernel_{int8,bf16} (attention.hpp:536-652)."""
@@ -38,6 +43,7 @@ class OracleDecoder:
             if p < 0 or (not ring and p >= self.caps[l]):
                 continue
             r = p % cfg.sliding_window if ring else p
+            self.kc[l][b, r], self.vc[l][b, r] = k[b], v[b]
             self.kq[l][b, r], self.ks[l][b, r] = kq[b], ks[b]
             self.vq[l][b, r], self.vs[l][b, r] = vq[b], vs[b]
             if l % 2 == 1 and p < cfg.keep:
@@ -55,11 +61,16 @@ class OracleDecoder:
         q = rq if q is None else q
         self.kv_update(l, rk if k is None else k, rv if v is None else v, pos)
         keep = cfg.keep if l % 2 == 1 else 0
-        o32 = oracle.attn_decode(q, self.kq[l], self.vq[l], self.ks[l], self.vs[l],
-                                 self.kb[l] if keep else None, self.vb[l] if keep else None,
-                                 w["sinks"][l], pos, n_kv_heads=8, layer_idx=l,
-                                 sliding_window=cfg.sliding_window, keep=cfg.keep,
-                                 prefix_rule=cfg.prefix_rule)
+        if self.bf16_cache:
+            o32 = oracle.attn_decode(q, None, None, None, None, self.kc[l], self.vc[l], w["sinks"][l], pos,
+                                     n_kv_heads=8, layer_idx=l, sliding_window=cfg.sliding_window, keep=0,
+                                     cache_bf16=True)
+        else:
+            o32 = oracle.attn_decode(q, self.kq[l], self.vq[l], self.ks[l], self.vs[l],
+                                     self.kb[l] if keep else None, self.vb[l] if keep else None,
+                                     w["sinks"][l], pos, n_kv_heads=8, layer_idx=l,
+                                     sliding_window=cfg.sliding_window, keep=cfg.keep,
+                                     prefix_rule=cfg.prefix_rule)
         from synth import f32_to_bf16
         out["o"] = o = f32_to_bf16(o32)
         out["proj"] = proj = oracle.matmul_bf16(o.reshape(self.B, -1), w["w_o"][l])

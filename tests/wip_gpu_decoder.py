@@ -89,10 +89,14 @@ def test_decoder_ops_match_oracle(model):
                 assert np.array_equal(bk, ref.kb[l][b]) and np.array_equal(bv, ref.vb[l][b])
 
 
-def test_decoder_end_to_end(model):
+@pytest.mark.parametrize("kind", [ga.CACHE_INT8, ga.CACHE_BF16])
+def test_decoder_end_to_end(model, kind):
+    """Both cache kinds: C4's int8 cache and the 20B path's bf16 rows."""
+    import dataclasses
+    cfg = dataclasses.replace(CFG, cache_kind=kind)
     w, moe = model
-    gpu = dec.from_host(CFG, B, w, moe)
-    ref = OracleDecoder(CFG, B, w, moe)
+    gpu = dec.from_host(cfg, B, w, moe)
+    ref = OracleDecoder(cfg, B, w, moe)
     rng = np.random.default_rng(12)
     tokens = rng.integers(0, CFG.vocab, size=(STEPS, B)).astype(np.int32)
     for s in range(STEPS):
@@ -102,7 +106,7 @@ def test_decoder_end_to_end(model):
     torch.cuda.synchronize()
     got = gpu.logits.view(torch.int16).cpu().numpy().view(np.uint16)
     m = parity.compare(got, want)
-    parity.RECORD.append({"what": "decoder end to end, last step", **{k: m[k] for k in ("max_abs", "max_abs_norm", "rel_l2", "frac_exact")}})
+    parity.RECORD.append({"what": f"decoder end to end, last step, cache kind {kind}", **{k: m[k] for k in ("max_abs", "max_abs_norm", "rel_l2", "frac_exact")}})
     assert m["finite"] and m["rel_l2"] <= 5e-2, m
 
 
