@@ -42,6 +42,9 @@ def parse():
                     help="skip the C4 MoE-share and attention lines (24 layers at 512 tokens)")
     ap.add_argument("--attn-only", action="store_true",
                     help="only the C4 attention line (decode attention over the int8 KV cache)")
+    ap.add_argument("--attn-cache", choices=["int8", "bf16"], default="int8",
+                    help="KV cache of the attention line: C4's int8 codes, or the 20B reference "
+                         "path's bf16 rows (attention_gpu)")
     ap.add_argument("--decoder-only", action="store_true",
                     help="only the C4 decode-step line (24 layers, 512 sequences)")
     ap.add_argument("--c4-full", action="store_true",
@@ -298,7 +301,9 @@ def time_c4_attention(args, dev):
     import torch
     import gptoss_attn as ga
     B, L, ctx, W, keep = 512, 24, 1024, 128, 128
-    kc = ga.KvCache(B, L, ctx, sliding_window=W, keep=keep, prefix_rule=ga.PREFIX_MIXED, device=dev)
+    bf = getattr(args, "attn_cache", "int8") == "bf16"
+    kc = ga.KvCache(B, L, ctx, sliding_window=W, keep=keep, prefix_rule=ga.PREFIX_MIXED, device=dev,
+                    cache_kind=ga.CACHE_BF16 if bf else ga.CACHE_INT8)
     g = torch.Generator(device=dev)
     g.manual_seed(0xA77E)
     pool = [(torch.randn((B, ga.KV_DIM), generator=g, device=dev).to(torch.bfloat16),
@@ -336,12 +341,15 @@ def time_c4_attention(args, dev):
     ms_decode = timed(lambda: step(False), steps)
     ms_odd = timed(lambda: kc.decode(1, q, sinks[1], pos, out=out), 20)
     ms_even = timed(lambda: kc.decode(0, q, sinks[0], pos, out=out), 20)
-    b_odd = attn_layer_bytes(B, ctx, keep)
-    b_even = attn_layer_bytes(B, W, 0)
+    b_odd = attn_layer_bytes(B, ctx, ctx if bf else keep)
+    b_even = attn_layer_bytes(B, W, W if bf else 0)
     b_step = (L // 2) * (b_odd + b_even)
     gbs = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 1)
+    what = "bf16 KV cache (the 20B reference path)" if bf else \
+        "int8 KV cache, 128 bf16 tokens on odd layers"
     return {"workload": "c4 attention share: 24 x (KV update + decode attention), 512 sequences, "
-                        "context 1024, window 128 on even layers, 128 bf16 tokens on odd layers",
+                        "context 1024, window 128 on even layers, " + what,
+            "cache": "bf16" if bf else "int8",
             "ms_per_step": round(ms_step, 4), "decode_only_ms_per_step": round(ms_decode, 4),
             "tokens_per_s": round(B / (ms_step * 1e-3), 1), "steps": steps,
             "odd_layer_us": round(ms_odd * 1e3, 2), "even_layer_us": round(ms_even * 1e3, 2),
