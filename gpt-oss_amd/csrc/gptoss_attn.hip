@@ -471,13 +471,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3, 8))) void
         // layer's rows of the sequence (the same base kv_update_kernel writes)
         const size_t slab = a.bf16cache ? (size_t)b * a.bks + a.lko
                                         : ((size_t)b * a.n_layers + a.layer) * a.keep * kKvDim;
-        for (int blk = blk0; blk < e16; blk += 2) {
-            const int nb = min(2, e16 - blk);
-            BlkBf A, B;
-            load_bf(a, slab, kvh, blk, c, g, A);
-            if (nb > 1) load_bf(a, slab, kvh, blk + 1, c, g, B);
-            else B = A;  // not used: its rows are masked
-            pair_bf(A, B, blk, nb, nvalid, g, q0, q1, st);
+        // Two register buffers, one pair ahead: the next pair's loads are in
+        // flight while this pair computes.  Block indices are clamped to the
+        // last block, so every load is of a valid block (a partner past the
+        // end is masked by nb, a pair past the end is never computed), and no
+        // buffer is ever copied (a copy would wait for its loads).
+        auto load_pair = [&](int blk, BlkBf &X, BlkBf &Y) {
+            load_bf(a, slab, kvh, min(blk, e16 - 1), c, g, X);
+            load_bf(a, slab, kvh, min(blk + 1, e16 - 1), c, g, Y);
+        };
+        BlkBf A0, B0, A1, B1;
+        load_pair(blk0, A0, B0);
+        for (int blk = blk0; blk < e16; blk += 4) {
+            load_pair(blk + 2, A1, B1);
+            pair_bf(A0, B0, blk, min(2, e16 - blk), nvalid, g, q0, q1, st);
+            if (blk + 2 >= e16) break;
+            load_pair(blk + 4, A0, B0);
+            pair_bf(A1, B1, blk + 2, min(2, e16 - blk - 2), nvalid, g, q0, q1, st);
         }
     }
     const int i0 = max(blk0, nb16);
