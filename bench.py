@@ -417,17 +417,24 @@ def time_c4_decoder(args, dev):
 
 
 def time_variants(layers, x, out, fi, fw, args, c, flops):
-    """Extra measured variants (never the headline): the block-scaled FP4 MFMA
+    """Extra measured variants (never the headline): the streamed GEMM with
+    128-row tiles (bit-identical to the default) and the per-expert tile
+    switch (bf16, within the layer tolerance), then the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
     bf16 oracle) and one term.  Same workload, same weight rotation, the
     scaled-MFMA packing built once per copy outside the timed region."""
     import statistics
     import torch
-    for L in layers:
-        L.pack_fp4()
     out_v = {}
-    for path, note in (("fp4", "MXFP8 activations, hi + lo terms"),
+    flags = {"prefill": "GPTOSS_MOE_FLAG_PREFILL_TILES", "switch": "GPTOSS_MOE_FLAG_TILE_SWITCH",
+             "fp4": "GPTOSS_MOE_FLAG_FP4_MFMA", "fp4_fp8": "GPTOSS_MOE_FLAG_FP4_MFMA | GPTOSS_MOE_FLAG_FP8_ACT"}
+    for path, note in (("prefill", "bf16, 128-row tiles on the streamed GEMM"),
+                       ("switch", "bf16, experts of 128+ rows on the large-M GEMM"),
+                       ("fp4", "MXFP8 activations, hi + lo terms"),
                        ("fp4_fp8", "MXFP8 activations, hi term only")):
+        if path == "fp4":
+            for L in layers:
+                L.pack_fp4()
         for i in range(args.warmup):
             layers[i % len(layers)].forward(x, out, fi, fw, path=path)
         torch.cuda.synchronize()
@@ -443,8 +450,7 @@ def time_variants(layers, x, out, fi, fw, args, c, flops):
             r = layers[i % len(layers)].forward_profiled(x, out, fi, fw, path=path)
             for k, v in r.items():
                 prof[k].append(v)
-        out_v[path] = {"flag": "GPTOSS_MOE_FLAG_FP4_MFMA" + (" | GPTOSS_MOE_FLAG_FP8_ACT" if path == "fp4_fp8" else ""),
-                       "activations": note, "ms_per_step": round(ms, 5),
+        out_v[path] = {"flag": flags[path], "arithmetic": note, "ms_per_step": round(ms, 5),
                        "tokens_per_s": round(c.tokens / (ms * 1e-3), 1),
                        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
                        "kernel_ms": {k: round(statistics.median(v), 5) for k, v in prof.items()}}

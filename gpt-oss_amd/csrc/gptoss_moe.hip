@@ -2366,10 +2366,10 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
 //   waves 8, 9   weight producers: nontemporal global -> LDS loads (1 KB per
 //                instruction) of the item's packed nibbles (8 column tiles
 //                each), the stage's e8m0 block (wave 8) and the item's biases
-//                and row slots (wave 9), kSDW - 1 stages ahead.
+//                and row slots (wave 9), SDepth<R>::W - 1 stages ahead.
 //   waves 10, 11 activation producers: global -> LDS loads of the tile's
 //                activation rows (32 rows each, x rows by token for MLP1),
-//                kSDA - 1 stages ahead.
+//                SDepth<R>::A - 1 stages ahead.
 // A stage is 128 k of one item.  Iteration s: each producer waits until its
 // own loads of stage s have landed (exact per-wave counts: the number of
 // loads a producer issues per stage varies with the item), one s_barrier for
@@ -2381,26 +2381,39 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
 // flattened sequence; its Gx workgroups take equal contiguous ranges of it
 // (cut at tile ends and at 8 units), so every CU streams the same number of
 // weight bytes whatever N / 256 is (MLP2's 2880 rows are 11.25 blocks of 256).
+// R, the rows of a tile, is 64 (decode; the default) or 128 (prefill: each
+// weight element is converted once for twice the rows, streamed once for
+// them, and a stage carries twice the MFMAs per barrier).  With R = 128 the
+// rings are 3 deep (the activation slot is 32 KB), consumers hold 8 x 2
+// accumulator fragments, and each activation producer loads 64 rows.
 constexpr int kSK = 128;        // k per stage
 constexpr int kSCons = 8;       // consumer waves
 constexpr int kSThreads = 12 * 64;
-constexpr int kSDW = 5;         // weight ring stages
-constexpr int kSDA = 4;         // activation ring stages
 constexpr int kSUnits = 8;      // weight units (32 rows) per item, at most
+template <int R>
+struct SDepth {
+    static_assert(R == 64 || R == 128, "tile rows");
+    static constexpr int W = R == 64 ? 5 : 3;  // weight ring stages
+    static constexpr int A = R == 64 ? 4 : 3;  // activation ring stages
+};
 
-struct SWSlot {
+template <int R>
+struct SWSlotR {
     uint4 w[16][64];        // column tile j of the item: its packed 1 KB block for the stage
     uint4 sc[64];           // e8m0 of the stage: tile j, row n at byte 64 j + 4 n (4 k groups)
     uint16_t bias[512];     // (item's last stage) biases of weight rows 32 f .. 32 (f + cnt) - 1
-    int32_t slot[64];       // (item's last stage, MLP2) token-order slot of tile row r
+    int32_t slot[R];        // (item's last stage, MLP2) token-order slot of tile row r
 };
-struct SASlot {
-    uint4 a[64 * 16];       // tile row r, 16-byte unit u (k 8u..8u+7) at r * 16 + (u ^ (r & 15))
+template <int R>
+struct SASlotR {
+    uint4 a[R * 16];        // tile row r, 16-byte unit u (k 8u..8u+7) at r * 16 + (u ^ (r & 15))
 };
-struct SShared {
-    SWSlot w[kSDW];
-    SASlot a[kSDA];
+template <int R>
+struct SSharedR {
+    SWSlotR<R> w[SDepth<R>::W];
+    SASlotR<R> a[SDepth<R>::A];
 };
+static_assert(sizeof(SSharedR<64>) <= 160 * 1024 && sizeof(SSharedR<128>) <= 160 * 1024, "LDS");
 
 // s_waitcnt vmcnt(n) for a run-time n (wave-uniform): the instruction takes
 // an immediate, so branch to it.
@@ -2488,9 +2501,9 @@ struct SCursor {
 // product: lane n + 16 g holds weight rows 4 g .. 4 g + 3 of column tile t
 // against tile row 16 m + n (the epilogue then owns 4 consecutive output
 // columns of one row per lane).
-template <int MT, int NKS>
-__device__ __forceinline__ void s_compute(const SWSlot &ws, const SASlot &as, int c,
-                                          f32x4 (&acc)[4][2]) {
+template <int MT, int NKS, int R>
+__device__ __forceinline__ void s_compute(const SWSlotR<R> &ws, const SASlotR<R> &as, int c,
+                                          f32x4 (&acc)[R / 16][2]) {
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     u32x4 wv[2];
     uint32_t sc[2];
@@ -2520,15 +2533,57 @@ __device__ __forceinline__ void s_compute(const SWSlot &ws, const SASlot &as, in
     }
 }
 
+// The 128-row tiles' stage in one code path (a path per row count would
+// make the compiler copy all 64 accumulator registers where the paths meet):
+// row groups m < mt and k steps ks < nks, both wave-uniform guards; one k
+// step at a time (hoisting the next steps' conversions and operand reads
+// would not fit the registers).
+template <int R>
+__device__ __forceinline__ void s_compute_dyn(const SWSlotR<R> &ws, const SASlotR<R> &as, int c, int mt,
+                                              int nks, f32x4 (&acc)[R / 16][2]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    u32x4 wv[2];
+    uint32_t sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        wv[t] = *reinterpret_cast<const u32x4 *>(&ws.w[2 * c + t][lane]);
+        sc[t] = reinterpret_cast<const uint32_t *>(ws.sc)[(2 * c + t) * 16 + n];
+    }
+    const char *arow = reinterpret_cast<const char *>(as.a) + n * 256;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        if (ks < nks) {
+            bf16x8 b[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t e = (sc[t] >> (8 * ks)) & 0xffu;
+                const uint32_t q = wv[t][ks] & (e == 0 ? 0x88888888u : 0xffffffffu);
+                b[t] = dequant8(q, e8m0_to_f32(e));
+            }
+            const int uo = ((4 * ks + g) ^ n) * 16;
+#pragma unroll
+            for (int m = 0; m < R / 16; ++m) {
+                if (m < mt) {
+                    const bf16x8 a =
+                        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(arow + m * 4096 + uo));
+                    acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[0], a, acc[m][0], 0, 0, 0);
+                    acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[1], a, acc[m][1], 0, 0, 0);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Epilogue of consumer c (acc as s_compute leaves it: lane n + 16 g, tile
 // row 16 m + n, weight rows 4 g + v of tiles 0 and 1).  MLP1: tile 0 holds
 // the gate rows and tile 1 the up rows of output columns 16 (f + c) .. + 15,
 // so the lane's 4 outputs 16 (f + c) + 4 g + v are adjacent: one 8-byte
 // store per row.  MLP2: tile t holds output columns 32 (f + c) + 16 t + 4 g
 // + v: two 8-byte stores per row into its token-order slot.
-template <int MT, bool kMlp1>
-__device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlot &ws, const Tile &tl,
-                                           int f, int c, const f32x4 (&acc)[4][2]) {
+template <int MT, bool kMlp1, int R>
+__device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlotR<R> &ws, const Tile &tl,
+                                           int f, int c, const f32x4 (&acc)[R / 16][2]) {
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int N = a.N;
     if (kMlp1) {
@@ -2578,9 +2633,46 @@ __device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlot &ws, 
     }
 }
 
-template <bool kMlp1>
+// One stage of consumer c for a tile of mt 16-row groups (1 .. R / 16): the
+// stage's MFMAs, then on the item's last stage the epilogue and a reset.
+template <bool kMlp1, int R, int MT>
+__device__ __forceinline__ void s_stage_mt(const GemmArgs &a, const SWSlotR<R> &ws, const SASlotR<R> &as,
+                                           const SCursor &cur, int c, bool half, bool last,
+                                           f32x4 (&acc)[R / 16][2]) {
+    if (half) s_compute<MT, 2, R>(ws, as, c, acc);
+    else s_compute<MT, 4, R>(ws, as, c, acc);
+    if (last) {
+        s_epilogue<MT, kMlp1, R>(a, ws, cur.tl, cur.f, c, acc);
+#pragma unroll
+        for (int m = 0; m < R / 16; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+template <bool kMlp1, int R>
+__device__ __forceinline__ void s_stage(const GemmArgs &a, const SWSlotR<R> &ws, const SASlotR<R> &as,
+                                        const SCursor &cur, int c, int mt, bool half, bool last,
+                                        f32x4 (&acc)[R / 16][2]) {
+    if constexpr (R == 128) {
+        s_compute_dyn<R>(ws, as, c, mt, half ? 2 : 4, acc);
+        if (last) {
+            s_epilogue<R / 16, kMlp1, R>(a, ws, cur.tl, cur.f, c, acc);  // rows past tl.rows skipped
+#pragma unroll
+            for (int m = 0; m < R / 16; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        return;
+    }
+    switch (mt) {
+        case 1: s_stage_mt<kMlp1, R, 1>(a, ws, as, cur, c, half, last, acc); break;
+        case 2: s_stage_mt<kMlp1, R, 2>(a, ws, as, cur, c, half, last, acc); break;
+        case 3: s_stage_mt<kMlp1, R, 3>(a, ws, as, cur, c, half, last, acc); break;
+        default: s_stage_mt<kMlp1, R, 4>(a, ws, as, cur, c, half, last, acc); break;
+    }
+}
+
+template <bool kMlp1, int R>
 __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
-    __shared__ SShared sh;
+    constexpr int kDW = SDepth<R>::W, kDA = SDepth<R>::A;
+    constexpr int kPR = R / 2;  // activation rows per producer
+    __shared__ SSharedR<R> sh;
     const GemmArgs &a = d.g;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -2596,37 +2688,16 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
 
     if (wave < kSCons) {
         // ------------------------------------------------ consumers
-        f32x4 acc[4][2];
+        f32x4 acc[R / 16][2];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < R / 16; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         const bool half_k = (K % kSK) != 0;  // the last stage holds 64 k
         for (int s = 0; cur.valid(); ++s, cur.next()) {
             s_barrier_mem();
-            const SWSlot &ws = sh.w[s % kSDW];
-            const SASlot &as = sh.a[s % kSDA];
             const int mt = (cur.tl.rows + 15) >> 4;
             const bool last = cur.kp == KP - 1;
-            if (wave < cur.cnt) {
-                if (last && half_k) {
-                    if (mt <= 1) s_compute<1, 2>(ws, as, wave, acc);
-                    else if (mt == 2) s_compute<2, 2>(ws, as, wave, acc);
-                    else if (mt == 3) s_compute<3, 2>(ws, as, wave, acc);
-                    else s_compute<4, 2>(ws, as, wave, acc);
-                } else {
-                    if (mt <= 1) s_compute<1, 4>(ws, as, wave, acc);
-                    else if (mt == 2) s_compute<2, 4>(ws, as, wave, acc);
-                    else if (mt == 3) s_compute<3, 4>(ws, as, wave, acc);
-                    else s_compute<4, 4>(ws, as, wave, acc);
-                }
-                if (last) {
-                    if (mt <= 1) s_epilogue<1, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
-                    else if (mt == 2) s_epilogue<2, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
-                    else if (mt == 3) s_epilogue<3, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
-                    else s_epilogue<4, kMlp1>(a, ws, cur.tl, cur.f, wave, acc);
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-            }
+            if (wave < cur.cnt)
+                s_stage<kMlp1, R>(a, sh.w[s % kDW], sh.a[s % kDA], cur, wave, mt, last && half_k, last, acc);
         }
         return;
     }
@@ -2639,12 +2710,12 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
     // stages are outstanding).
     const bool wprod = wave < kSCons + 2;
     const int p = wprod ? wave - kSCons : wave - kSCons - 2;  // 0 / 1
-    const int depth = wprod ? kSDW : kSDA;
+    const int depth = wprod ? kDW : kDA;
     uint64_t ring = 0;
     int issued = 0, done = 0, is = 0;
     SCursor icur = cur;  // issue cursor
     const uint32_t lane16 = 16u * (uint32_t)lane;
-    uint32_t aoff[8];    // activation producers: byte offset of load i's 16 bytes (from A)
+    uint32_t aoff[kPR / 4];  // activation producers: byte offset of load i's 16 bytes (from A)
     int ng = 0;          // activation producers: 16-row groups this wave loads for the item
     uint32_t soff = 0;   // weight producer 0: byte offset of this lane's scales (from the stage's row)
     const char *Ab = reinterpret_cast<const char *>(a.A);
@@ -2657,26 +2728,31 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
             return;
         }
         const int mt = (tl.rows + 15) >> 4;
-        ng = min(max(mt - 2 * p, 0), 2);
+        ng = min(max(mt - (kPR / 16) * p, 0), kPR / 16);
         if (ng == 0) return;
-        const int rlim = tl.rows - 1 - 32 * p;  // last valid row of this wave's 32, relative
+        const int rlim = tl.rows - 1 - kPR * p;  // last valid row of this wave's kPR, relative
         const int q = lane >> 4;
-        int rowv = 0;  // lane j < 32: activation row of item row 32 p + j (unclamped)
+        int rowv = 0;  // lane j < kPR: activation row of item row kPR p + j (unclamped)
         if (d.a_token != nullptr) {
-            // the 32 tokens as scalars, spread over lanes 0..31
-            const ConstInts rt = (ConstInts)(d.a_token + tl.row0 + 32 * p);
-            int tk[32];
+            // the tokens as scalars (scalar loads: not counted by vmcnt), 32 at a
+            // time, spread over lanes 0 .. kPR - 1; rows past the tile repeat
+            // its last token (the tile list never ends a tile past offsets[E])
+            const ConstInts rt = (ConstInts)(d.a_token + tl.row0 + kPR * p);
 #pragma unroll
-            for (int j = 0; j < 32; ++j) tk[j] = rt[j];
+            for (int h = 0; h < kPR / 32; ++h) {
+                int tk[32];
 #pragma unroll
-            for (int j = 0; j < 32; ++j)
-                asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(rowv) : "s"(tk[j]), "n"(j));
+                for (int j = 0; j < 32; ++j) tk[j] = rt[min(32 * h + j, max(rlim, 0))];
+#pragma unroll
+                for (int j = 0; j < 32; ++j)
+                    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(rowv) : "s"(tk[j]), "n"(32 * h + j));
+            }
         } else {
-            rowv = tl.row0 + 32 * p + (lane & 31);
+            rowv = tl.row0 + kPR * p + (lane & (kPR - 1));
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int rel = min(4 * i + q, rlim);              // clamped row within the 32
+        for (int i = 0; i < kPR / 4; ++i) {
+            const int rel = min(4 * i + q, rlim);              // clamped row within the kPR
             const int row = __shfl(rowv, rel);
             const int u = (lane & 15) ^ ((4 * i + q) & 15);   // the LDS position's k unit
             aoff[i] = (uint32_t)row * (uint32_t)(2 * K) + 16u * (uint32_t)u;
@@ -2688,7 +2764,7 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
         const Tile &tl = c.tl;
         if (c.kp == 0) item_setup(c);
         if (wprod) {
-            SWSlot &ws = sh.w[st % kSDW];
+            SWSlotR<R> &ws = sh.w[st % kDW];
             const int ntile = 2 * c.cnt;
             const int j1 = min(8 * p + 8, ntile);
             // tile j's block for this stage: ((e CT + 2 f + j) KP + kp) KB
@@ -2710,21 +2786,24 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
                 ++n_ld;
                 if (!kMlp1) {
                     const char *rs = reinterpret_cast<const char *>(a.row_slot + tl.row0);
-                    lds_dma4(rs + 4u * (uint32_t)min(lane, tl.rows - 1), &ws.slot[0]);
-                    ++n_ld;
+#pragma unroll
+                    for (int h = 0; h < R / 64; ++h) {
+                        lds_dma4(rs + 4u * (uint32_t)min(64 * h + lane, tl.rows - 1), &ws.slot[64 * h]);
+                        ++n_ld;
+                    }
                 }
             }
         } else if (ng > 0) {
-            SASlot &as = sh.a[st % kSDA];
+            SASlotR<R> &as = sh.a[st % kDA];
             const char *ab = Ab + (size_t)c.kp * (2 * kSK);
             const bool half = c.kp * kSK + kSK > K;  // only k units 0..7 exist
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kPR / 4; ++i) {
                 if (i < 4 * ng) {
                     uint32_t o = aoff[i];
                     // past K: reread unit u - 8 of the row (in bounds; never computed on)
                     if (half && ((lane & 15) ^ ((4 * i + (lane >> 4)) & 15)) >= 8) o -= 128u;
-                    lds_dma16(ab + o, &as.a[(32 * p + 4 * i) * 16]);
+                    lds_dma16(ab + o, &as.a[(kPR * p + 4 * i) * 16]);
                     ++n_ld;
                 }
             }
@@ -3029,7 +3108,8 @@ bool shape_ok(const gptoss_moe_shape *s) {
 
 constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SMALL_M_GEMM |
                                GPTOSS_MOE_FLAG_LARGE_M_GEMM | GPTOSS_MOE_FLAG_FP4_MFMA |
-                               GPTOSS_MOE_FLAG_FP8_ACT | GPTOSS_MOE_FLAG_TILE_SWITCH;
+                               GPTOSS_MOE_FLAG_FP8_ACT | GPTOSS_MOE_FLAG_TILE_SWITCH |
+                               GPTOSS_MOE_FLAG_PREFILL_TILES;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -3192,11 +3272,16 @@ int switch_rows(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, u
     return GPTOSS_MOE_TILE_SWITCH_ROWS;
 }
 
-// Rows per tile of the tile list: the direct GEMM takes whole decode experts,
-// up to 64 rows; the LDS-staged GEMM 32 (the large-M GEMM builds its own).
+// Rows per tile of the streamed GEMM: 128 with GPTOSS_MOE_FLAG_PREFILL_TILES,
+// else 64 (whole decode experts).  No call picks 128 by itself yet: the
+// choice from T * top_k / E waits for its measurement.
+int stream_rows(unsigned flags) { return (flags & GPTOSS_MOE_FLAG_PREFILL_TILES) ? 128 : kDTileRows; }
+
+// Rows per tile of the tile list: the streamed GEMM's (above), the FP4
+// variant's 64, the LDS-staged GEMM's 32 (the large-M GEMM builds its own).
 int gemm_tile_rows(const gptoss_moe_shape *s, const gptoss_moe_weights *w, int T, unsigned flags) {
     const GemmPath p = gemm_path(s, w, T, flags);
-    return p == PATH_DIRECT || p == PATH_FP4 ? kDTileRows : kTileRows;
+    return p == PATH_DIRECT ? stream_rows(flags) : p == PATH_FP4 ? kDTileRows : kTileRows;
 }
 
 // Expert weights and flags of a forward call.  The streamed GEMM (packed set,
@@ -3266,9 +3351,12 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         hipLaunchKernelGGL((large_m_gemm_kernel<true, false>), dim3(cap), dim3(kLWaves * 64), 0, st, a1,
                            p.counts, p.offsets, s->n_experts, LPacked{nullptr, nullptr, nullptr, 0});
     else if (direct) {
-        hipLaunchKernelGGL(stream_gemm_kernel<true>, dim3(cap), dim3(kSThreads), 0, st,
-                           SArgs{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1),
-                                 w->packed + PL.s1, p.row_token});
+        const SArgs sa{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1), w->packed + PL.s1,
+                       p.row_token};
+        if (stream_rows(flags) == 128)
+            hipLaunchKernelGGL((stream_gemm_kernel<true, 128>), dim3(cap), dim3(kSThreads), 0, st, sa);
+        else
+            hipLaunchKernelGGL((stream_gemm_kernel<true, 64>), dim3(cap), dim3(kSThreads), 0, st, sa);
         if (big < INT_MAX)  // the experts the streamed GEMM's tile list left out
             hipLaunchKernelGGL((large_m_gemm_kernel<true, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a1x,
                                p.counts, p.offsets, s->n_experts,
@@ -3302,9 +3390,11 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         hipLaunchKernelGGL((large_m_gemm_kernel<false, false>), dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                            p.counts, p.offsets, s->n_experts, LPacked{nullptr, nullptr, nullptr, 0});
     else if (direct) {
-        hipLaunchKernelGGL(stream_gemm_kernel<false>, dim3(cap), dim3(kSThreads), 0, st,
-                           SArgs{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2),
-                                 w->packed + PL.s2, nullptr});
+        const SArgs sa{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2), w->packed + PL.s2, nullptr};
+        if (stream_rows(flags) == 128)
+            hipLaunchKernelGGL((stream_gemm_kernel<false, 128>), dim3(cap), dim3(kSThreads), 0, st, sa);
+        else
+            hipLaunchKernelGGL((stream_gemm_kernel<false, 64>), dim3(cap), dim3(kSThreads), 0, st, sa);
         if (big < INT_MAX)
             hipLaunchKernelGGL((large_m_gemm_kernel<false, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                                p.counts, p.offsets, s->n_experts,

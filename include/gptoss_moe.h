@@ -70,6 +70,14 @@ extern "C" {
  * hidden, intermediate >= 256; ignored without packed weights. */
 #define GPTOSS_MOE_FLAG_TILE_SWITCH 32u
 #define GPTOSS_MOE_TILE_SWITCH_ROWS 128
+/* 128-row tiles on the streamed GEMM (packed weights; prefill): each expert's
+ * rows are cut into tiles of up to 128 rows instead of 64, so each weight
+ * element is streamed and converted once per 128 rows and a pipeline stage
+ * carries twice the MFMAs.  Same k order per output as the 64-row tiles:
+ * results are bit-identical to the default.  Ignored without packed weights
+ * or with SMALL_M / LARGE_M / FP4_MFMA.  (The reference's 32x32 path is
+ * chosen for a whole call from its largest count, getp_run.cpp:2666.) */
+#define GPTOSS_MOE_FLAG_PREFILL_TILES 64u
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {

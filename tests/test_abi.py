@@ -79,7 +79,7 @@ def test_argument_errors_without_gpu():
                                 64, 8, None) == gm.ERR_WORKSPACE
     # unknown flag bits; the FP4 variant's flags without its weights or combined wrongly
     need = gm.workspace_size(s, 8)
-    for flags in (64, gm.FLAG_FP4_MFMA, gm.FLAG_FP8_ACT,
+    for flags in (128, gm.FLAG_FP4_MFMA, gm.FLAG_FP8_ACT,
                   gm.FLAG_FP4_MFMA | gm.FLAG_SMALL_M_GEMM):
         assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
                                       flags, fake, need, 8, None) == gm.ERR_INVALID_ARG, flags

@@ -101,37 +101,68 @@ def test_weight_scale_bias_loads_in_bounds(N, K):
                 assert np.array_equal(np.sort(first[:4 * cnt]) - e * N, 32 * f + 8 * np.arange(4 * cnt))
 
 
-def act_dma(rows, K, kp, p, row0, token=None):
-    """item_setup + issue(), activation producer p: for each of its loads i,
-    the source element offset of every lane (from A) and the LDS unit it
-    fills; rows past the tile repeat its last row, and in a 64-k stage
-    (K % 128 == 64, last kp) units 8..15 reread units 0..7."""
+def act_dma(rows, K, kp, p, row0, token=None, R=64):
+    """item_setup + issue(), activation producer p of the R-row kernel (it
+    loads R / 2 rows): for each of its loads i, the source element offset of
+    every lane (from A) and the LDS unit it fills; rows past the tile repeat
+    its last row, and in a 64-k stage (K % 128 == 64, last kp) units 8..15
+    reread units 0..7."""
+    PR = R // 2
     mt = (rows + 15) >> 4
-    ng = min(max(mt - 2 * p, 0), 2)
-    rlim = rows - 1 - 32 * p
+    ng = min(max(mt - (PR // 16) * p, 0), PR // 16)
+    rlim = rows - 1 - PR * p
     q = LANE >> 4
     half = kp * SK + SK > K
     out = []
     for i in range(4 * ng):
         rel = np.minimum(4 * i + q, rlim)
-        r_item = 32 * p + rel                    # clamped tile row
+        r_item = PR * p + rel                    # clamped tile row
         row = token[row0 + r_item] if token is not None else row0 + r_item
         u = (LANE & 15) ^ ((4 * i + q) & 15)
         o = row * (2 * K) + 16 * u + kp * 2 * SK
         if half:
             o = np.where(u >= 8, o - 128, o)
-        lds_unit = (32 * p + 4 * i) * 16 + LANE
+        lds_unit = (PR * p + 4 * i) * 16 + LANE
         out.append((o, lds_unit, r_item, u))
     return out
 
 
+def token_reads(rows, p, R=64):
+    """item_setup's scalar reads of the row tokens (producer p, MLP1): the
+    indices (relative to the tile's row0) of the reads that fill lanes
+    0 .. R / 2 - 1, 32 at a time, each clamped to the tile's last row."""
+    PR = R // 2
+    rlim = rows - 1 - PR * p
+    return [PR * p + min(32 * h + j, max(rlim, 0)) for h in range(PR // 32) for j in range(32)]
+
+
+@pytest.mark.parametrize("R", [64, 128])
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 96, 127, 128])
+def test_token_reads_stay_in_the_tile(R, rows):
+    if rows > R:
+        pytest.skip("tile larger than R")
+    for p in (0, 1):
+        PR = R // 2
+        mt = (rows + 15) >> 4
+        if min(max(mt - (PR // 16) * p, 0), PR // 16) == 0:
+            continue  # the producer loads nothing for this tile (returns before reading)
+        idx = token_reads(rows, p, R)
+        assert min(idx) >= 0 and max(idx) <= rows - 1
+        # the lanes that rows use get their own row's token
+        for j in range(min(PR, rows - PR * p)):
+            assert idx[j] == PR * p + j
+
+
+@pytest.mark.parametrize("R", [64, 128])
 @pytest.mark.parametrize("K", [64, 128, 448, 2880, 3072])
-@pytest.mark.parametrize("rows", [1, 15, 16, 17, 32, 33, 48, 63, 64])
-def test_activation_loads(K, rows):
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 32, 33, 48, 63, 64, 65, 80, 97, 127, 128])
+def test_activation_loads(K, rows, R):
     """Every activation load stays inside its source row (bytes of row `row`
     only), every LDS unit of the row groups the MFMAs read is written exactly
     once per stage, and the unit at LDS position r * 16 + (U ^ (r & 15))
     holds row r's k unit U (the consumer's read form)."""
+    if rows > R:
+        pytest.skip("tile larger than R")
     KP = -(-K // SK)
     T = 300
     rng = np.random.default_rng(rows * 7 + K)
@@ -139,16 +170,17 @@ def test_activation_loads(K, rows):
     row0 = 5
     mt = (rows + 15) >> 4
     for kp in range(KP):
-        written = np.full(64 * 16, -1, np.int64)
+        written = np.full(R * 16, -1, np.int64)
         for p in (0, 1):
             for tok in (None, token):
-                for o, unit, r_item, u in act_dma(rows, K, kp, p, row0, tok):
+                for o, unit, r_item, u in act_dma(rows, K, kp, p, row0, tok, R):
                     src_row = tok[row0 + r_item] if tok is not None else row0 + r_item
                     assert (o >= src_row * 2 * K).all() and (o + 16 <= (src_row + 1) * 2 * K).all()
                     assert (o % 16 == 0).all()
                     if tok is None:
+                        assert (written[unit] == -1).all()   # once per stage
                         written[unit] = o
-                    assert unit.max() < 64 * 16
+                    assert unit.max() < R * 16
         # coverage of the MFMA row groups
         need = 16 * mt
         assert (written[:need * 16] >= 0).all()
@@ -162,9 +194,9 @@ def test_activation_loads(K, rows):
 
 
 def test_token_scalar_reads_stay_in_workspace():
-    """item_setup reads 32 row tokens per activation producer without
-    clamping (rows past the tile are never used): the furthest index,
-    row0 + 63 with row0 + rows <= P, must stay inside the workspace."""
+    """item_setup's row-token reads are clamped to the tile (above), so the
+    furthest index is P - 1; this also holds for the unclamped bound of an
+    earlier form, row0 + 63 with row0 + rows <= P."""
     lib = gm.load_library()
     for H, D, E, k, T in ((2880, 2880, 32, 4, 256), (128, 128, 4, 2, 1), (128, 128, 4, 1, 1),
                           (2880, 2880, 128, 4, 1), (256, 256, 8, 8, 3)):
@@ -182,12 +214,14 @@ def test_token_scalar_reads_stay_in_workspace():
         assert furthest <= v.act - base
 
 
-def test_lds_layout_fits():
-    """Weight ring 5 x (16 tiles x 1 KB + 1 KB scales + 1 KB biases + 256 B
-    slots) + activation ring 4 x 16 KB fits gfx950's 160 KB."""
-    wslot = 16 * 1024 + 1024 + 1024 + 256
-    aslot = 64 * 256
-    assert 5 * wslot + 4 * aslot <= 160 * 1024
+@pytest.mark.parametrize("R,dw,da", [(64, 5, 4), (128, 3, 3)])
+def test_lds_layout_fits(R, dw, da):
+    """Weight ring dw x (16 tiles x 1 KB + 1 KB scales + 1 KB biases + R
+    slots of 4 B) + activation ring da x R rows of 256 B fits gfx950's
+    160 KB (the kernel's static_assert checks the same sizes)."""
+    wslot = 16 * 1024 + 1024 + 1024 + 4 * R
+    aslot = R * 256
+    assert dw * wslot + da * aslot <= 160 * 1024
 
 
 def mfma_transposed_acc(w_tiles, x_rows, MT):
@@ -196,7 +230,7 @@ def mfma_transposed_acc(w_tiles, x_rows, MT):
     operand, so D_t = W_t . X^T (16 weight rows x 16 tile rows per group m),
     and lane n + 16 g holds D_t rows 4 g .. 4 g + 3 of column n.  Returns
     acc[lane][m][t][v]."""
-    acc = np.zeros((64, 4, 2, 4), np.float32)
+    acc = np.zeros((64, max(MT, 1), 2, 4), np.float32)
     for m in range(MT):
         xm = np.zeros((16, x_rows.shape[1]), np.float32)
         blk = x_rows[16 * m:16 * m + 16]
@@ -217,7 +251,7 @@ def swiglu(gt, up, alpha=1.702, limit=7.0):
 
 
 @pytest.mark.parametrize("mlp1", [True, False])
-@pytest.mark.parametrize("rows", [1, 5, 16, 17, 37, 64])
+@pytest.mark.parametrize("rows", [1, 5, 16, 17, 37, 64, 65, 100, 128])
 def test_epilogue_lane_columns(mlp1, rows):
     """s_epilogue on the transposed accumulators: every output element of
     the tile's rows is written once, by the lane and 8-byte store the kernel
@@ -234,7 +268,7 @@ def test_epilogue_lane_columns(mlp1, rows):
     n_out_rows = row0 + rows + 3
     out = np.full((n_out_rows, D), np.nan, np.float32)
     writes = np.zeros((n_out_rows, D), np.int64)
-    slot = rng.permutation(n_out_rows)[:64]          # MLP2: token-order slot of tile row r
+    slot = rng.permutation(n_out_rows)[:rows]        # MLP2: token-order slot of tile row r
     pr = np.arange(N)
     src = ((pr & ~31) + 2 * (pr & 15) + ((pr >> 4) & 1)) if mlp1 else pr  # packed row -> weight row
     wb = bias[32 * f:32 * (f + cnt)]                   # the item's biases in the ring slot (weight-row order)
@@ -273,3 +307,20 @@ def test_epilogue_lane_columns(mlp1, rows):
     assert (wr == 1).all()
     assert writes.sum() == wr.size                      # nothing else written
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("R", [64, 128])
+@pytest.mark.parametrize("rows", [1, 2, 63, 64, 65, 127, 128])
+def test_slot_loads(R, rows):
+    """MLP2's row slots on the item's last stage: R / 64 four-byte loads per
+    lane, load h lane l reading tile row min(64 h + l, rows - 1) into slot
+    entry 64 h + l, so entries 0 .. rows - 1 hold their own row's slot and no
+    read leaves the tile."""
+    if rows > R:
+        pytest.skip("tile larger than R")
+    slot = np.full(R, -1)
+    for h in range(R // 64):
+        src = np.minimum(64 * h + LANE, rows - 1)
+        assert src.max() <= rows - 1
+        slot[64 * h + LANE] = src
+    assert np.array_equal(slot[:rows], np.arange(rows))
