@@ -49,6 +49,9 @@ def parse():
                     help="only the C4 decode-step line (24 layers, 512 sequences)")
     ap.add_argument("--c4-full", action="store_true",
                     help="also the C4 attention and decode-step lines in a full run")
+    ap.add_argument("--new-variants", action="store_true",
+                    help="also the 128-row-tile and tile-switch variant lines (kernels whose GPU "
+                         "tests have not passed yet)")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -428,10 +431,11 @@ def time_variants(layers, x, out, fi, fw, args, c, flops):
     out_v = {}
     flags = {"prefill": "GPTOSS_MOE_FLAG_PREFILL_TILES", "switch": "GPTOSS_MOE_FLAG_TILE_SWITCH",
              "fp4": "GPTOSS_MOE_FLAG_FP4_MFMA", "fp4_fp8": "GPTOSS_MOE_FLAG_FP4_MFMA | GPTOSS_MOE_FLAG_FP8_ACT"}
-    for path, note in (("prefill", "bf16, 128-row tiles on the streamed GEMM"),
-                       ("switch", "bf16, experts of 128+ rows on the large-M GEMM"),
-                       ("fp4", "MXFP8 activations, hi + lo terms"),
-                       ("fp4_fp8", "MXFP8 activations, hi term only")):
+    paths = [("fp4", "MXFP8 activations, hi + lo terms"), ("fp4_fp8", "MXFP8 activations, hi term only")]
+    if getattr(args, "new_variants", False):
+        paths = [("prefill", "bf16, 128-row tiles on the streamed GEMM"),
+                 ("switch", "bf16, experts of 128+ rows on the large-M GEMM")] + paths
+    for path, note in paths:
         if path == "fp4":
             for L in layers:
                 L.pack_fp4()
