@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--c4-full", action="store_true",
                     help="also the C4 attention and decode-step lines in a full run")
     ap.add_argument("--new-variants", action="store_true",
-                    help="also the 128-row-tile and tile-switch variant lines (kernels whose GPU "
+                    help="also the prefetching-consumer, 128-row-tile and tile-switch variant lines (kernels whose GPU "
                          "tests have not passed yet)")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
@@ -421,7 +421,8 @@ def time_c4_decoder(args, dev):
 
 def time_variants(layers, x, out, fi, fw, args, c, flops):
     """Extra measured variants (never the headline): the streamed GEMM with
-    128-row tiles (bit-identical to the default) and the per-expert tile
+    prefetching consumers or 128-row tiles (both bit-identical to the
+    default) and the per-expert tile
     switch (bf16, within the layer tolerance), then the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
     bf16 oracle) and one term.  Same workload, same weight rotation, the
@@ -430,10 +431,12 @@ def time_variants(layers, x, out, fi, fw, args, c, flops):
     import torch
     out_v = {}
     flags = {"prefill": "GPTOSS_MOE_FLAG_PREFILL_TILES", "switch": "GPTOSS_MOE_FLAG_TILE_SWITCH",
+             "prefetch": "GPTOSS_MOE_FLAG_STAGE_PREFETCH",
              "fp4": "GPTOSS_MOE_FLAG_FP4_MFMA", "fp4_fp8": "GPTOSS_MOE_FLAG_FP4_MFMA | GPTOSS_MOE_FLAG_FP8_ACT"}
     paths = [("fp4", "MXFP8 activations, hi + lo terms"), ("fp4_fp8", "MXFP8 activations, hi term only")]
     if getattr(args, "new_variants", False):
-        paths = [("prefill", "bf16, 128-row tiles on the streamed GEMM"),
+        paths = [("prefetch", "bf16, prefetching consumers on the streamed GEMM"),
+                 ("prefill", "bf16, 128-row tiles on the streamed GEMM"),
                  ("switch", "bf16, experts of 128+ rows on the large-M GEMM")] + paths
     for path, note in paths:
         if path == "fp4":

@@ -2481,6 +2481,11 @@ struct SCursor {
         }
     }
     __device__ __forceinline__ bool valid() const { return left > 0; }
+    // kSync: wait for the tile's scalar loads right where they are issued (a
+    // tile change), so that the compiler's own wait for them (lgkmcnt(0),
+    // which also drains every LDS read in flight) is not placed on the path
+    // that every stage takes
+    template <bool kSync = false>
     __device__ __forceinline__ void next() {
         if (++kp < KP) return;
         kp = 0;
@@ -2489,7 +2494,10 @@ struct SCursor {
         if (f == UPT) {
             f = 0;
             ++t;
-            if (left > 0) load_tile();
+            if (left > 0) {
+                load_tile();
+                if (kSync) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            }
         }
         if (left > 0) set_cnt();
     }
@@ -2581,7 +2589,9 @@ __device__ __forceinline__ void s_compute_dyn(const SWSlotR<R> &ws, const SASlot
 // so the lane's 4 outputs 16 (f + c) + 4 g + v are adjacent: one 8-byte
 // store per row.  MLP2: tile t holds output columns 32 (f + c) + 16 t + 4 g
 // + v: two 8-byte stores per row into its token-order slot.
-template <int MT, bool kMlp1, int R>
+// kTight: one row group at a time (a scheduling fence after each), so that
+// the compiler does not interleave all of them and overrun the registers.
+template <int MT, bool kMlp1, int R, bool kTight = false>
 __device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlotR<R> &ws, const Tile &tl,
                                            int f, int c, const f32x4 (&acc)[R / 16][2]) {
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -2609,6 +2619,7 @@ __device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlotR<R> &
                 *reinterpret_cast<uint2 *>(a.out_act + (size_t)(tl.row0 + r) * D + j0) =
                     make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
             }
+            if constexpr (kTight) __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         const int h = 32 * (f + c) + 4 * g;
@@ -2629,6 +2640,7 @@ __device__ __forceinline__ void s_epilogue(const GemmArgs &a, const SWSlotR<R> &
                     *reinterpret_cast<uint2 *>(dst + 16 * t) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
                 }
             }
+            if constexpr (kTight) __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
@@ -2668,8 +2680,196 @@ __device__ __forceinline__ void s_stage(const GemmArgs &a, const SWSlotR<R> &ws,
     }
 }
 
-template <bool kMlp1, int R>
+// The prefetching consumer (GPTOSS_MOE_FLAG_STAGE_PREFETCH, R = 64): the
+// k steps of a consumer's stages form one stream, and the operands of k step
+// ks sit in register set ks & 1, read two k steps ahead (every stage holds an
+// even number of k steps, so the parity never changes).  A set holds, for
+// k step ks of one stage: per column tile t the lane's nibble word (dword ks
+// of its 16-byte entry) and e8m0 word (byte ks is the step's), and the
+// activation fragments a[m] (tile row 16 m + n, k unit 4 ks + g) for m < mt.
+//
+// The reads are inline-asm LDS loads into the set's registers in place, so
+// a set read only for m < mt keeps one register home (compiled loads under
+// such guards made the compiler copy every set where the guards join).  The
+// compiler does not see these loads, so each use waits for them explicitly:
+// LDS returns in issue order, and when k step j starts, the only LDS reads
+// of this wave issued after set j's are those of set j + 1, so
+// lgkmcnt(ops of set j + 1) means set j has landed.  Scalar loads, which also
+// count in lgkmcnt, only make that wait stricter.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+struct SKReg {
+    u32x2 w, sc;
+    u32x4 a[4];
+};
+
+__device__ __forceinline__ uint32_t lds_addr32(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Read k step ks of a stage (weight slot at LDS byte wslot, activation slot
+// at aslot) into r, row groups m < mt (0 <= mt <= 4; mt = 0 reads nothing):
+// 2 + mt LDS instructions, the activation reads last.  Returns their count.
+__device__ __forceinline__ int s_read_k(uint32_t wslot, uint32_t aslot, int c, int ks, int mt, SKReg &r,
+                                        int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    const uint32_t wa = wslot + (uint32_t)offsetof(SWSlotR<64>, w) +
+                        (uint32_t)((2 * c * 64 + lane) * 16 + 4 * ks);                    // tile 1: + 1 KB
+    const uint32_t sa = wslot + (uint32_t)offsetof(SWSlotR<64>, sc) + 4u * (uint32_t)((2 * c) * 16 + n);  // tile 1: + 64 B
+    const uint32_t aa = aslot + (uint32_t)(n * 256 + ((4 * ks + g) ^ n) * 16);
+    asm volatile(
+        "s_cmp_eq_u32 %9, 0\n\t"
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"
+        "ds_read2st64_b32 %0, %6 offset1:4\n\t"
+        "ds_read2_b32 %1, %7 offset1:16\n\t"
+        "ds_read_b128 %2, %8\n\t"
+        "s_cmp_lt_u32 %9, 2\n\t"
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"
+        "ds_read_b128 %3, %8 offset:4096\n\t"
+        "s_cmp_lt_u32 %9, 3\n\t"
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"
+        "ds_read_b128 %4, %8 offset:8192\n\t"
+        "s_cmp_lt_u32 %9, 4\n\t"
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"
+        "ds_read_b128 %5, %8 offset:12288\n"
+        ".Lsrk_done%=:"
+        : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3])
+        : "v"(wa), "v"(sa), "v"(aa), "s"(mt)
+        : "scc");
+    return mt > 0 ? 2 + mt : 0;
+}
+
+// Wait for set r.  The set was read before the last set issued, if any
+// (rd = that set's operations, 0 if none): every set is at least 3
+// operations, and LDS returns in issue order, so lgkmcnt(3) means r has
+// landed (at the cost of the later set's first operation), and lgkmcnt(0)
+// when no later set was issued.  Only the second wait carries r's registers
+// (so that their uses stay below it), and it is unconditional: the sets keep
+// one definition per k step.
+__device__ __forceinline__ void s_wait_set(SKReg &r, int rd) {
+    if (rd == 0) asm volatile("s_waitcnt lgkmcnt(0)");
+    asm volatile("s_waitcnt lgkmcnt(3)"
+                 : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3]));
+}
+
+// One k step from register set r: conversion of the two column tiles'
+// nibbles, then the MFMAs of row groups m < MT.
+template <int MT>
+__device__ __forceinline__ void s_k_step_mt(const SKReg &r, int ks, f32x4 (&acc)[4][2]) {
+    bf16x8 b[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t e = (r.sc[t] >> (8 * ks)) & 0xffu;
+        // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
+        const uint32_t q = r.w[t] & (e == 0 ? 0x88888888u : 0xffffffffu);
+        b[t] = dequant8(q, e8m0_to_f32(e));
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const bf16x8 a = __builtin_bit_cast(bf16x8, r.a[m]);
+        acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[0], a, acc[m][0], 0, 0, 0);
+        acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[1], a, acc[m][1], 0, 0, 0);
+    }
+}
+// One stage of the prefetching consumer c with MT row groups and NKS k
+// steps.  On entry set ks & 1 holds k step ks of this stage for ks = 0, 1,
+// and rd = the LDS operations of the last set read; on exit the sets hold k
+// steps 0, 1 of the next stage when nxt (the next stage is the same item's).
+// Slot j computes k step j, then reads into the same set the k step two
+// ahead in the stream: with NKS = 4 slots 0, 1 read k steps 2, 3 of this
+// stage (slots w0 / a0) and slots 2, 3 k steps 0, 1 of the next (w1 / a1).
+template <int MT, int NKS>
+__device__ __forceinline__ void s_stage_pre(SKReg (&r)[2], int &rd, bool nxt, uint32_t w0, uint32_t a0,
+                                            uint32_t w1, uint32_t a1, int c, int lane, f32x4 (&acc)[4][2]) {
+#pragma unroll
+    for (int j = 0; j < NKS; ++j) {
+        s_wait_set(r[j & 1], rd);
+        __builtin_amdgcn_sched_barrier(0);
+        s_k_step_mt<MT>(r[j & 1], j, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (NKS == 4 && j < 2) rd = s_read_k(w0, a0, c, j + 2, MT, r[j & 1], lane);
+        else rd = s_read_k(w1, a1, c, j - (NKS - 2), nxt ? MT : 0, r[j & 1], lane);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The stages of one item for the prefetching consumer c with MT row groups
+// (MT = 0: the wave has no weight unit in this item and only keeps the
+// barriers): register sets and accumulators local to the item (k steps 0, 1
+// of its first stage read cold), the epilogue after the last stage.  s = the
+// stage index of the item's first stage, whose barrier has passed; on return
+// cur and s stand at the next item and its first barrier has passed.
+// Returns false when no stage is left.
+template <bool kMlp1, int MT, bool kHalf>
+__device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<64> &sh, SCursor &cur, int &s,
+                                           int KP, int c) {
+    constexpr int kDW = SDepth<64>::W, kDA = SDepth<64>::A;
+    const uint32_t wbase = lds_addr32(&sh.w[0]), abase = lds_addr32(&sh.a[0]);
+    // the lane through an opaque move: the read addresses derived from it are
+    // built inside the item, not hoisted out of the item loop for every item
+    // variant at once (that alone overran the register budget)
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    SKReg r[2];
+    int rd = 0;
+    f32x4 acc[4][2];
+    if constexpr (MT > 0) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
+        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
+        s_read_k(w0, a0, c, 0, MT, r[0], lane);
+        rd = s_read_k(w0, a0, c, 1, MT, r[1], lane);
+    }
+    // stages 0 .. KP - 2 of the item: four k steps each, the next stage's
+    // first two read ahead
+    for (int kp = 0; kp < KP - 1; ++kp) {
+        if constexpr (MT > 0) {
+            const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
+            const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
+            const uint32_t w1 = wbase + (uint32_t)(((s + 1) % kDW) * sizeof(SWSlotR<64>));
+            const uint32_t a1 = abase + (uint32_t)(((s + 1) % kDA) * sizeof(SASlotR<64>));
+            s_stage_pre<MT, 4>(r, rd, true, w0, a0, w1, a1, c, lane, acc);
+        }
+        cur.next<true>();
+        ++s;
+        s_barrier_mem();
+    }
+    // the last stage (64 k when kHalf: K % 128 != 0), then the epilogue
+    if constexpr (MT > 0) {
+        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
+        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
+        s_stage_pre<MT, kHalf ? 2 : 4>(r, rd, false, w0, a0, w0, a0, c, lane, acc);
+        s_epilogue<MT, kMlp1, 64, true>(a, sh.w[s % kDW], cur.tl, cur.f, c, acc);
+    }
+    cur.next<true>();
+    ++s;
+    if (!cur.valid()) return false;
+    s_barrier_mem();
+    return true;
+}
+
+// The prefetching consumer c over all its items (kHalf: the last stage of
+// an item holds 64 k).
+template <bool kMlp1, bool kHalf>
+__device__ __forceinline__ void s_consume_pre(const GemmArgs &a, SSharedR<64> &sh, SCursor &cur, int KP,
+                                              int c) {
+    int s = 0;
+    s_barrier_mem();
+    for (bool more = true; more;) {
+        const int mt = c < cur.cnt ? (cur.tl.rows + 15) >> 4 : 0;
+        switch (mt) {
+            case 0: more = s_item_pre<kMlp1, 0, kHalf>(a, sh, cur, s, KP, c); break;
+            case 1: more = s_item_pre<kMlp1, 1, kHalf>(a, sh, cur, s, KP, c); break;
+            case 2: more = s_item_pre<kMlp1, 2, kHalf>(a, sh, cur, s, KP, c); break;
+            case 3: more = s_item_pre<kMlp1, 3, kHalf>(a, sh, cur, s, KP, c); break;
+            default: more = s_item_pre<kMlp1, 4, kHalf>(a, sh, cur, s, KP, c); break;
+        }
+    }
+}
+
+template <bool kMlp1, int R, bool kPre>
 __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
+    static_assert(!kPre || R == 64, "the prefetching consumer holds at most 4 row groups");
     constexpr int kDW = SDepth<R>::W, kDA = SDepth<R>::A;
     constexpr int kPR = R / 2;  // activation rows per producer
     __shared__ SSharedR<R> sh;
@@ -2692,6 +2892,16 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
 #pragma unroll
         for (int m = 0; m < R / 16; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         const bool half_k = (K % kSK) != 0;  // the last stage holds 64 k
+        if constexpr (kPre) {
+            // Barrier s certifies stages s and s + 1 (the producers wait one
+            // stage further ahead) and slot s stays intact until barrier
+            // s + 1.  The barrier that opens stage s + 1 closes stage s.
+            // One dispatch per item on its row groups (a guard per row group
+            // made the compiler copy and spill the accumulators).
+            if (half_k) s_consume_pre<kMlp1, true>(a, sh, cur, KP, wave);
+            else s_consume_pre<kMlp1, false>(a, sh, cur, KP, wave);
+            return;
+        } else {
         for (int s = 0; cur.valid(); ++s, cur.next()) {
             s_barrier_mem();
             const int mt = (cur.tl.rows + 15) >> 4;
@@ -2700,6 +2910,7 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
                 s_stage<kMlp1, R>(a, sh.w[s % kDW], sh.a[s % kDA], cur, wave, mt, last && half_k, last, acc);
         }
         return;
+        }
     }
 
     // ---------------------------------------------------- producers
@@ -2813,9 +3024,13 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
     };
 
     for (; is < depth - 1 && icur.valid(); ++is, icur.next()) issue(is, icur);
+    int counted = 0;  // stages whose loads are in `done`
     for (int s = 0; s < is; ++s) {
-        done += (int)((ring >> (8 * (s & 7))) & 0xff);
-        wait_vmcnt_dyn(issued - done);  // this wave's loads of stage s have landed
+        // this wave's loads of stage s (and with kPre of stage s + 1, issued
+        // since the ring is at least 3 deep) have landed
+        for (; counted <= (kPre ? s + 1 : s) && counted < is; ++counted)
+            done += (int)((ring >> (8 * (counted & 7))) & 0xff);
+        wait_vmcnt_dyn(issued - done);
         s_barrier_mem();
         if (icur.valid()) {
             issue(is, icur);
@@ -3109,7 +3324,7 @@ bool shape_ok(const gptoss_moe_shape *s) {
 constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SMALL_M_GEMM |
                                GPTOSS_MOE_FLAG_LARGE_M_GEMM | GPTOSS_MOE_FLAG_FP4_MFMA |
                                GPTOSS_MOE_FLAG_FP8_ACT | GPTOSS_MOE_FLAG_TILE_SWITCH |
-                               GPTOSS_MOE_FLAG_PREFILL_TILES;
+                               GPTOSS_MOE_FLAG_PREFILL_TILES | GPTOSS_MOE_FLAG_STAGE_PREFETCH;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -3354,9 +3569,11 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
         const SArgs sa{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1), w->packed + PL.s1,
                        p.row_token};
         if (stream_rows(flags) == 128)
-            hipLaunchKernelGGL((stream_gemm_kernel<true, 128>), dim3(cap), dim3(kSThreads), 0, st, sa);
+            hipLaunchKernelGGL((stream_gemm_kernel<true, 128, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
+        else if (flags & GPTOSS_MOE_FLAG_STAGE_PREFETCH)
+            hipLaunchKernelGGL((stream_gemm_kernel<true, 64, true>), dim3(cap), dim3(kSThreads), 0, st, sa);
         else
-            hipLaunchKernelGGL((stream_gemm_kernel<true, 64>), dim3(cap), dim3(kSThreads), 0, st, sa);
+            hipLaunchKernelGGL((stream_gemm_kernel<true, 64, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
         if (big < INT_MAX)  // the experts the streamed GEMM's tile list left out
             hipLaunchKernelGGL((large_m_gemm_kernel<true, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a1x,
                                p.counts, p.offsets, s->n_experts,
@@ -3392,9 +3609,11 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     else if (direct) {
         const SArgs sa{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2), w->packed + PL.s2, nullptr};
         if (stream_rows(flags) == 128)
-            hipLaunchKernelGGL((stream_gemm_kernel<false, 128>), dim3(cap), dim3(kSThreads), 0, st, sa);
+            hipLaunchKernelGGL((stream_gemm_kernel<false, 128, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
+        else if (flags & GPTOSS_MOE_FLAG_STAGE_PREFETCH)
+            hipLaunchKernelGGL((stream_gemm_kernel<false, 64, true>), dim3(cap), dim3(kSThreads), 0, st, sa);
         else
-            hipLaunchKernelGGL((stream_gemm_kernel<false, 64>), dim3(cap), dim3(kSThreads), 0, st, sa);
+            hipLaunchKernelGGL((stream_gemm_kernel<false, 64, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
         if (big < INT_MAX)
             hipLaunchKernelGGL((large_m_gemm_kernel<false, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                                p.counts, p.offsets, s->n_experts,

@@ -32,13 +32,15 @@ FLAG_FP4_MFMA = 8
 FLAG_FP8_ACT = 16
 FLAG_TILE_SWITCH = 32
 FLAG_PREFILL_TILES = 64
+FLAG_STAGE_PREFETCH = 128
 # "fp4": block-scaled FP4 MFMA on MXFP8 activations (hi + lo terms); "fp4_fp8":
 # the same with the hi term only.  Both need the packed_fp4 weights (pack_fp4()).
 # "switch": the packed path with the per-expert tile switch (experts of >= 128
 # rows on the large-M GEMM's 128-row tiles).
 _PATH_FLAGS = {"auto": 0, "small": FLAG_SMALL_M_GEMM, "large": FLAG_LARGE_M_GEMM,
                "fp4": FLAG_FP4_MFMA, "fp4_fp8": FLAG_FP4_MFMA | FLAG_FP8_ACT,
-               "switch": FLAG_TILE_SWITCH, "prefill": FLAG_PREFILL_TILES}
+               "switch": FLAG_TILE_SWITCH, "prefill": FLAG_PREFILL_TILES,
+               "prefetch": FLAG_STAGE_PREFETCH}
 
 _ERRNAMES = {ERR_INVALID_ARG: "invalid argument", ERR_WORKSPACE: "workspace too small",
              ERR_HIP: "HIP error", ERR_UNSUPPORTED: "unsupported shape"}
@@ -360,8 +362,8 @@ class MoeLayer:
         """e_agg (or out + e_agg with residual=True) for bf16 rows x_norm [T][H].
         path: "auto", "small" / "large" to force a grouped-GEMM path,
         "switch" for the per-expert tile switch on packed weights, "prefill"
-        for 128-row tiles on the streamed GEMM, or
-        "fp4" / "fp4_fp8" for the block-scaled FP4 MFMA variant."""
+        for 128-row tiles on the streamed GEMM, "prefetch" for its prefetching
+        consumers, or "fp4" / "fp4_fp8" for the block-scaled FP4 MFMA variant."""
         import torch
         T = x_norm.shape[0]
         if out is None:

@@ -78,6 +78,14 @@ extern "C" {
  * or with SMALL_M / LARGE_M / FP4_MFMA.  (The reference's 32x32 path is
  * chosen for a whole call from its largest count, getp_run.cpp:2666.) */
 #define GPTOSS_MOE_FLAG_PREFILL_TILES 64u
+/* Prefetching consumers on the streamed GEMM (packed weights, 64-row
+ * tiles): each consumer wave reads the next pipeline stage's operands from
+ * LDS into registers while the current stage's MFMAs run, instead of reading
+ * each operand just before its use; the producers then wait for their loads
+ * one stage earlier.  Same MFMAs in the same k order: results are
+ * bit-identical to the default.  Ignored with PREFILL_TILES and on the other
+ * GEMM paths.  No counterpart in the reference (a schedule, not a result). */
+#define GPTOSS_MOE_FLAG_STAGE_PREFETCH 128u
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {
