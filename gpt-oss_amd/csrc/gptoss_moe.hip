@@ -2693,9 +2693,9 @@ __device__ __forceinline__ void s_stage(const GemmArgs &a, const SWSlotR<R> &ws,
 // such guards made the compiler copy every set where the guards join).  The
 // compiler does not see these loads, so each use waits for them explicitly:
 // LDS returns in issue order, and when k step j starts, the only LDS reads
-// of this wave issued after set j's are those of set j + 1, so
-// lgkmcnt(ops of set j + 1) means set j has landed.  Scalar loads, which also
-// count in lgkmcnt, only make that wait stricter.
+// of this wave issued after set j's are those of set j + 1 (at least two
+// operations), so lgkmcnt(2) means set j has landed.  Scalar loads, which
+// also count in lgkmcnt, only make that wait stricter.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 struct SKReg {
     u32x2 w, sc;
@@ -2707,8 +2707,12 @@ __device__ __forceinline__ uint32_t lds_addr32(const void *p) {
 }
 
 // Read k step ks of a stage (weight slot at LDS byte wslot, activation slot
-// at aslot) into r, row groups m < mt (0 <= mt <= 4; mt = 0 reads nothing):
-// 2 + mt LDS instructions, the activation reads last.  Returns their count.
+// at aslot) into r, row groups m < mt (0 <= mt <= 4; mt = 0 reads nothing).
+// The e8m0 words hold all four k steps of a stage, so they are read only
+// with k steps 0 and 1 (kSc), the first read of a stage into each set; k
+// steps 2 and 3 keep them.  1 + kSc + mt LDS instructions, the activation
+// reads last.  Returns their count.
+template <bool kSc>
 __device__ __forceinline__ int s_read_k(uint32_t wslot, uint32_t aslot, int c, int ks, int mt, SKReg &r,
                                         int lane) {
     const int n = lane & 15, g = lane >> 4;
@@ -2716,38 +2720,51 @@ __device__ __forceinline__ int s_read_k(uint32_t wslot, uint32_t aslot, int c, i
                         (uint32_t)((2 * c * 64 + lane) * 16 + 4 * ks);                    // tile 1: + 1 KB
     const uint32_t sa = wslot + (uint32_t)offsetof(SWSlotR<64>, sc) + 4u * (uint32_t)((2 * c) * 16 + n);  // tile 1: + 64 B
     const uint32_t aa = aslot + (uint32_t)(n * 256 + ((4 * ks + g) ^ n) * 16);
-    asm volatile(
-        "s_cmp_eq_u32 %9, 0\n\t"
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"
-        "ds_read2st64_b32 %0, %6 offset1:4\n\t"
-        "ds_read2_b32 %1, %7 offset1:16\n\t"
-        "ds_read_b128 %2, %8\n\t"
-        "s_cmp_lt_u32 %9, 2\n\t"
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"
-        "ds_read_b128 %3, %8 offset:4096\n\t"
-        "s_cmp_lt_u32 %9, 3\n\t"
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"
-        "ds_read_b128 %4, %8 offset:8192\n\t"
-        "s_cmp_lt_u32 %9, 4\n\t"
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"
-        "ds_read_b128 %5, %8 offset:12288\n"
+#define SRK_ACT                                          \
+        "ds_read_b128 %2, %8\n\t"                        \
+        "s_cmp_lt_u32 %9, 2\n\t"                         \
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"                \
+        "ds_read_b128 %3, %8 offset:4096\n\t"            \
+        "s_cmp_lt_u32 %9, 3\n\t"                         \
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"                \
+        "ds_read_b128 %4, %8 offset:8192\n\t"            \
+        "s_cmp_lt_u32 %9, 4\n\t"                         \
+        "s_cbranch_scc1 .Lsrk_done%=\n\t"                \
+        "ds_read_b128 %5, %8 offset:12288\n"             \
         ".Lsrk_done%=:"
-        : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3])
-        : "v"(wa), "v"(sa), "v"(aa), "s"(mt)
-        : "scc");
-    return mt > 0 ? 2 + mt : 0;
+    if constexpr (kSc)
+        asm volatile(
+            "s_cmp_eq_u32 %9, 0\n\t"
+            "s_cbranch_scc1 .Lsrk_done%=\n\t"
+            "ds_read2st64_b32 %0, %6 offset1:4\n\t"
+            "ds_read2_b32 %1, %7 offset1:16\n\t"
+            SRK_ACT
+            : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3])
+            : "v"(wa), "v"(sa), "v"(aa), "s"(mt)
+            : "scc");
+    else
+        asm volatile(
+            "s_cmp_eq_u32 %9, 0\n\t"
+            "s_cbranch_scc1 .Lsrk_done%=\n\t"
+            "ds_read2st64_b32 %0, %6 offset1:4\n\t"
+            SRK_ACT
+            : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3])
+            : "v"(wa), "v"(sa), "v"(aa), "s"(mt)
+            : "scc");
+#undef SRK_ACT
+    return mt > 0 ? 1 + (kSc ? 1 : 0) + mt : 0;
 }
 
 // Wait for set r.  The set was read before the last set issued, if any
-// (rd = that set's operations, 0 if none): every set is at least 3
-// operations, and LDS returns in issue order, so lgkmcnt(3) means r has
-// landed (at the cost of the later set's first operation), and lgkmcnt(0)
+// (rd = that set's operations, 0 if none): every set is at least 2
+// operations, and LDS returns in issue order, so lgkmcnt(2) means r has
+// landed (at the cost of the later set's first operations), and lgkmcnt(0)
 // when no later set was issued.  Only the second wait carries r's registers
 // (so that their uses stay below it), and it is unconditional: the sets keep
 // one definition per k step.
 __device__ __forceinline__ void s_wait_set(SKReg &r, int rd) {
     if (rd == 0) asm volatile("s_waitcnt lgkmcnt(0)");
-    asm volatile("s_waitcnt lgkmcnt(3)"
+    asm volatile("s_waitcnt lgkmcnt(2)"
                  : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3]));
 }
 
@@ -2786,8 +2803,8 @@ __device__ __forceinline__ void s_stage_pre(SKReg (&r)[2], int &rd, bool nxt, ui
         __builtin_amdgcn_sched_barrier(0);
         s_k_step_mt<MT>(r[j & 1], j, acc);
         __builtin_amdgcn_sched_barrier(0);
-        if (NKS == 4 && j < 2) rd = s_read_k(w0, a0, c, j + 2, MT, r[j & 1], lane);
-        else rd = s_read_k(w1, a1, c, j - (NKS - 2), nxt ? MT : 0, r[j & 1], lane);
+        if (NKS == 4 && j < 2) rd = s_read_k<false>(w0, a0, c, j + 2, MT, r[j & 1], lane);
+        else rd = s_read_k<true>(w1, a1, c, j - (NKS - 2), nxt ? MT : 0, r[j & 1], lane);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -2817,8 +2834,8 @@ __device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<64> &sh, 
         for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
         const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
-        s_read_k(w0, a0, c, 0, MT, r[0], lane);
-        rd = s_read_k(w0, a0, c, 1, MT, r[1], lane);
+        s_read_k<true>(w0, a0, c, 0, MT, r[0], lane);
+        rd = s_read_k<true>(w0, a0, c, 1, MT, r[1], lane);
     }
     // stages 0 .. KP - 2 of the item: four k steps each, the next stage's
     // first two read ahead

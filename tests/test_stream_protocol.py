@@ -77,7 +77,7 @@ class LdsQueue:
         return self.ops - self.last_of[tag] >= n
 
 
-def consumer_pre(stages, KP, half, c, always_three=False):
+def consumer_pre(stages, KP, half, c, always_two=False):
     """The prefetching consumer c: a list of (phase, stage) reads with the
     phase their data is used in (returned by then), and the k steps it
     computes; asserts set contents and lgkmcnt coverage on the way."""
@@ -89,17 +89,23 @@ def consumer_pre(stages, KP, half, c, always_three=False):
     s = 0
     phase = 0  # s_barrier_mem() before the first item: phase 0
 
+    sc_of = [None, None]  # the stage whose e8m0 words a set holds
+
     def read_k(stage, ks, mt, p, ph):
-        n = 2 + mt if mt > 0 else 0
+        with_sc = ks < 2  # s_read_k<kSc>: only k steps 0, 1 read the e8m0 words
+        n = 1 + with_sc + mt if mt > 0 else 0
         if n:
             sets[p] = (stage, ks)
+            if with_sc:
+                sc_of[p] = stage
             q.read((stage, ks, p), n)
             reads.append((stage, ph))
         return n
 
     def use_set(p, stage, ks, rd_, ph):
         assert sets[p] == (stage, ks), (sets[p], stage, ks)
-        n = 3 if (rd_ > 0 or always_three) else 0
+        assert sc_of[p] == stage, (sc_of[p], stage)
+        n = 2 if (rd_ > 0 or always_two) else 0
         assert q.wait_covers((stage, ks, p), n)
         computed.append((stage, ks, ph))
 
@@ -234,10 +240,10 @@ def test_model_flags_an_unshifted_producer_wait():
         check_ring(stages, [(t, ph, t if t > ph else ph) for t, ph in reads], issue, landed, 5, True)
 
 
-def test_model_flags_lgkmcnt3_without_a_later_set():
-    # the last k step of an item has no later set in flight: lgkmcnt(3) there
+def test_model_flags_lgkmcnt2_without_a_later_set():
+    # the last k step of an item has no later set in flight: lgkmcnt(2) there
     # would not cover it
     stages = stages_of([(40, 8)], 3)
     consumer_pre(stages, 3, False, 0)
     with pytest.raises(AssertionError):
-        consumer_pre(stages, 3, False, 0, always_three=True)
+        consumer_pre(stages, 3, False, 0, always_two=True)
