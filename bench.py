@@ -421,8 +421,8 @@ def time_c4_decoder(args, dev):
 
 def time_variants(layers, x, out, fi, fw, args, c, flops):
     """Extra measured variants (never the headline): the streamed GEMM with
-    prefetching consumers or 128-row tiles (both bit-identical to the
-    default) and the per-expert tile
+    prefetching consumers (2 or 4 column tiles per wave) or 128-row tiles
+    (all bit-identical to the default) and the per-expert tile
     switch (bf16, within the layer tolerance), then the block-scaled FP4 MFMA
     path with MXFP8 activations, two terms (within the layer tolerance of the
     bf16 oracle) and one term.  Same workload, same weight rotation, the
@@ -431,11 +431,14 @@ def time_variants(layers, x, out, fi, fw, args, c, flops):
     import torch
     out_v = {}
     flags = {"prefill": "GPTOSS_MOE_FLAG_PREFILL_TILES", "switch": "GPTOSS_MOE_FLAG_TILE_SWITCH",
-             "prefetch": "GPTOSS_MOE_FLAG_STAGE_PREFETCH",
+             "prefetch": "GPTOSS_MOE_FLAG_STAGE_PREFETCH", "wide": "GPTOSS_MOE_FLAG_WIDE_CONSUMERS",
+             "wide_prefill": "GPTOSS_MOE_FLAG_WIDE_CONSUMERS | GPTOSS_MOE_FLAG_PREFILL_TILES",
              "fp4": "GPTOSS_MOE_FLAG_FP4_MFMA", "fp4_fp8": "GPTOSS_MOE_FLAG_FP4_MFMA | GPTOSS_MOE_FLAG_FP8_ACT"}
     paths = [("fp4", "MXFP8 activations, hi + lo terms"), ("fp4_fp8", "MXFP8 activations, hi term only")]
     if getattr(args, "new_variants", False):
         paths = [("prefetch", "bf16, prefetching consumers on the streamed GEMM"),
+                 ("wide", "bf16, wide prefetching consumers (4 column tiles per wave), 64-row tiles"),
+                 ("wide_prefill", "bf16, wide prefetching consumers, 128-row tiles"),
                  ("prefill", "bf16, 128-row tiles on the streamed GEMM"),
                  ("switch", "bf16, experts of 128+ rows on the large-M GEMM")] + paths
     for path, note in paths:

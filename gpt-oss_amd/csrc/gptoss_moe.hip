@@ -2387,8 +2387,6 @@ __global__ __launch_bounds__(kDWaves * 64) void direct_gemm_kernel(DArgs d) {
 // rings are 3 deep (the activation slot is 32 KB), consumers hold 8 x 2
 // accumulator fragments, and each activation producer loads 64 rows.
 constexpr int kSK = 128;        // k per stage
-constexpr int kSCons = 8;       // consumer waves
-constexpr int kSThreads = 12 * 64;
 constexpr int kSUnits = 8;      // weight units (32 rows) per item, at most
 template <int R>
 struct SDepth {
@@ -2680,113 +2678,143 @@ __device__ __forceinline__ void s_stage(const GemmArgs &a, const SWSlotR<R> &ws,
     }
 }
 
-// The prefetching consumer (GPTOSS_MOE_FLAG_STAGE_PREFETCH, R = 64): the
-// k steps of a consumer's stages form one stream, and the operands of k step
-// ks sit in register set ks & 1, read two k steps ahead (every stage holds an
-// even number of k steps, so the parity never changes).  A set holds, for
-// k step ks of one stage: per column tile t the lane's nibble word (dword ks
-// of its 16-byte entry) and e8m0 word (byte ks is the step's), and the
-// activation fragments a[m] (tile row 16 m + n, k unit 4 ks + g) for m < mt.
+// The prefetching consumers (GPTOSS_MOE_FLAG_STAGE_PREFETCH: 8 waves of
+// CT = 2 column tiles on 64-row tiles; GPTOSS_MOE_FLAG_WIDE_CONSUMERS: 4
+// waves of CT = 4 column tiles, on 64- or 128-row tiles).  The k steps of a
+// consumer's stages form one stream, and the operands of k step ks sit in
+// register set ks & 1, read two k steps ahead (every stage holds an even
+// number of k steps, so the parity never changes).  A set holds, for k step
+// ks of one stage: per column tile t the lane's nibble word (dword ks of its
+// 16-byte entry) and e8m0 word (byte ks is the step's), and the activation
+// fragments a[m] (tile row 16 m + n, k unit 4 ks + g) for m < mt.  With CT =
+// 4 each activation fragment feeds four MFMAs instead of two, which halves
+// the LDS reads per MFMA (each consumer re-reads the tile's activation rows).
 //
-// The reads are inline-asm LDS loads into the set's registers in place, so
-// a set read only for m < mt keeps one register home (compiled loads under
-// such guards made the compiler copy every set where the guards join).  The
-// compiler does not see these loads, so each use waits for them explicitly:
-// LDS returns in issue order, and when k step j starts, the only LDS reads
-// of this wave issued after set j's are those of set j + 1 (at least two
-// operations), so lgkmcnt(2) means set j has landed.  Scalar loads, which
-// also count in lgkmcnt, only make that wait stricter.
+// The reads are inline-asm LDS loads into the set's registers in place (each
+// behind its own wave-uniform skip inside the asm), so a set read only for
+// m < mt keeps one register home: compiled loads under such guards made the
+// compiler copy every set where the guards join.  The compiler does not see
+// these loads, so each use waits for them explicitly: LDS returns in issue
+// order, and when k step j starts, the only LDS reads of this wave issued
+// after set j's are those of set j + 1 (at least CT / 2 + 1 operations,
+// s_min_ops), so lgkmcnt(s_min_ops) means set j has landed.  Scalar loads,
+// which also count in lgkmcnt, only make that wait stricter.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <int R, int CT>
 struct SKReg {
-    u32x2 w, sc;
-    u32x4 a[4];
+    u32x2 w[CT / 2], sc[CT / 2];  // tiles 2 h, 2 h + 1
+    u32x4 a[R / 16];
 };
+template <int CT>
+constexpr int s_min_ops() { return CT / 2 + 1; }
 
 __device__ __forceinline__ uint32_t lds_addr32(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
+// ds_read2st64_b32 of dwords at addr + 256 * O0 and + 256 * O1, skipped when
+// mt == 0
+template <int O0, int O1>
+__device__ __forceinline__ void lds_read2st64_if(u32x2 &v, uint32_t addr, int mt) {
+    asm volatile("s_cmp_eq_u32 %2, 0\n\t"
+                 "s_cbranch_scc1 .Lr2s%=\n\t"
+                 "ds_read2st64_b32 %0, %1 offset0:%3 offset1:%4\n"
+                 ".Lr2s%=:"
+                 : "+v"(v) : "v"(addr), "s"(mt), "n"(O0), "n"(O1) : "scc");
+}
+// ds_read2_b32 of dwords at addr + 4 * O0 and + 4 * O1, skipped when mt == 0
+template <int O0, int O1>
+__device__ __forceinline__ void lds_read2_if(u32x2 &v, uint32_t addr, int mt) {
+    asm volatile("s_cmp_eq_u32 %2, 0\n\t"
+                 "s_cbranch_scc1 .Lr2%=\n\t"
+                 "ds_read2_b32 %0, %1 offset0:%3 offset1:%4\n"
+                 ".Lr2%=:"
+                 : "+v"(v) : "v"(addr), "s"(mt), "n"(O0), "n"(O1) : "scc");
+}
+// ds_read_b128 at addr + OFF, skipped when mt <= M
+template <int M, int OFF>
+__device__ __forceinline__ void lds_read_b128_if(u32x4 &v, uint32_t addr, int mt) {
+    asm volatile("s_cmp_le_u32 %2, %3\n\t"
+                 "s_cbranch_scc1 .Lr16%=\n\t"
+                 "ds_read_b128 %0, %1 offset:%4\n"
+                 ".Lr16%=:"
+                 : "+v"(v) : "v"(addr), "s"(mt), "n"(M), "n"(OFF) : "scc");
+}
+
+// The activation fragments of row groups M.. (< mt) of one k step, each
+// read with its offset as an immediate.
+template <int R, int M = 0>
+__device__ __forceinline__ void s_read_act(u32x4 (&a)[R / 16], uint32_t aa, int mt) {
+    if constexpr (M < R / 16) {
+        lds_read_b128_if<M, M * 4096>(a[M], aa, mt);
+        s_read_act<R, M + 1>(a, aa, mt);
+    }
+}
+
 // Read k step ks of a stage (weight slot at LDS byte wslot, activation slot
-// at aslot) into r, row groups m < mt (0 <= mt <= 4; mt = 0 reads nothing).
-// The e8m0 words hold all four k steps of a stage, so they are read only
-// with k steps 0 and 1 (kSc), the first read of a stage into each set; k
-// steps 2 and 3 keep them.  1 + kSc + mt LDS instructions, the activation
-// reads last.  Returns their count.
-template <bool kSc>
-__device__ __forceinline__ int s_read_k(uint32_t wslot, uint32_t aslot, int c, int ks, int mt, SKReg &r,
-                                        int lane) {
+// at aslot) into r, for consumer c's CT column tiles and row groups m < mt
+// (0 <= mt <= R / 16; mt = 0 reads nothing).  The e8m0 words hold all four
+// k steps of a stage, so they are read only with k steps 0 and 1 (kSc), the
+// first read of a stage into each set; k steps 2 and 3 keep them.
+// CT / 2 (1 + kSc) + mt LDS instructions, the activation reads last.
+// Returns their count.
+template <int R, int CT, bool kSc>
+__device__ __forceinline__ int s_read_k(uint32_t wslot, uint32_t aslot, int c, int ks, int mt,
+                                        SKReg<R, CT> &r, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const uint32_t wa = wslot + (uint32_t)offsetof(SWSlotR<64>, w) +
-                        (uint32_t)((2 * c * 64 + lane) * 16 + 4 * ks);                    // tile 1: + 1 KB
-    const uint32_t sa = wslot + (uint32_t)offsetof(SWSlotR<64>, sc) + 4u * (uint32_t)((2 * c) * 16 + n);  // tile 1: + 64 B
-    const uint32_t aa = aslot + (uint32_t)(n * 256 + ((4 * ks + g) ^ n) * 16);
-#define SRK_ACT                                          \
-        "ds_read_b128 %2, %8\n\t"                        \
-        "s_cmp_lt_u32 %9, 2\n\t"                         \
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"                \
-        "ds_read_b128 %3, %8 offset:4096\n\t"            \
-        "s_cmp_lt_u32 %9, 3\n\t"                         \
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"                \
-        "ds_read_b128 %4, %8 offset:8192\n\t"            \
-        "s_cmp_lt_u32 %9, 4\n\t"                         \
-        "s_cbranch_scc1 .Lsrk_done%=\n\t"                \
-        "ds_read_b128 %5, %8 offset:12288\n"             \
-        ".Lsrk_done%=:"
-    if constexpr (kSc)
-        asm volatile(
-            "s_cmp_eq_u32 %9, 0\n\t"
-            "s_cbranch_scc1 .Lsrk_done%=\n\t"
-            "ds_read2st64_b32 %0, %6 offset1:4\n\t"
-            "ds_read2_b32 %1, %7 offset1:16\n\t"
-            SRK_ACT
-            : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3])
-            : "v"(wa), "v"(sa), "v"(aa), "s"(mt)
-            : "scc");
-    else
-        asm volatile(
-            "s_cmp_eq_u32 %9, 0\n\t"
-            "s_cbranch_scc1 .Lsrk_done%=\n\t"
-            "ds_read2st64_b32 %0, %6 offset1:4\n\t"
-            SRK_ACT
-            : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3])
-            : "v"(wa), "v"(sa), "v"(aa), "s"(mt)
-            : "scc");
-#undef SRK_ACT
-    return mt > 0 ? 1 + (kSc ? 1 : 0) + mt : 0;
+    const uint32_t wa = wslot + (uint32_t)offsetof(SWSlotR<R>, w) +
+                        (uint32_t)((CT * c * 64 + lane) * 16 + 4 * ks);          // tile + 1: + 1 KB
+    const uint32_t sa = wslot + (uint32_t)offsetof(SWSlotR<R>, sc) +
+                        4u * (uint32_t)((CT * c) * 16 + n);                      // tile + 1: + 64 B
+    const uint32_t aa = aslot + (uint32_t)(n * 256 + ((4 * ks + g) ^ n) * 16);  // row group + 1: + 4 KB
+    lds_read2st64_if<0, 4>(r.w[0], wa, mt);
+    if constexpr (CT == 4) lds_read2st64_if<8, 12>(r.w[1], wa, mt);
+    if constexpr (kSc) {
+        lds_read2_if<0, 16>(r.sc[0], sa, mt);
+        if constexpr (CT == 4) lds_read2_if<32, 48>(r.sc[1], sa, mt);
+    }
+    s_read_act<R>(r.a, aa, mt);
+    return mt > 0 ? (CT / 2) * (kSc ? 2 : 1) + mt : 0;
 }
 
 // Wait for set r.  The set was read before the last set issued, if any
-// (rd = that set's operations, 0 if none): every set is at least 2
-// operations, and LDS returns in issue order, so lgkmcnt(2) means r has
-// landed (at the cost of the later set's first operations), and lgkmcnt(0)
-// when no later set was issued.  Only the second wait carries r's registers
-// (so that their uses stay below it), and it is unconditional: the sets keep
-// one definition per k step.
-__device__ __forceinline__ void s_wait_set(SKReg &r, int rd) {
+// (rd = that set's operations, 0 if none): every set is at least
+// s_min_ops<CT>() operations, and LDS returns in issue order, so
+// lgkmcnt(s_min_ops) means r has landed (at the cost of the later set's
+// first operations), and lgkmcnt(0) when no later set was issued.  Only the
+// second wait carries r's registers (so that their uses stay below it), and
+// it is unconditional: the sets keep one definition per k step.
+template <int R, int CT>
+__device__ __forceinline__ void s_wait_set(SKReg<R, CT> &r, int rd) {
     if (rd == 0) asm volatile("s_waitcnt lgkmcnt(0)");
-    asm volatile("s_waitcnt lgkmcnt(2)"
-                 : "+v"(r.w), "+v"(r.sc), "+v"(r.a[0]), "+v"(r.a[1]), "+v"(r.a[2]), "+v"(r.a[3]));
+    asm volatile("s_waitcnt lgkmcnt(%0)" : : "n"(s_min_ops<CT>()));
+#pragma unroll
+    for (int h = 0; h < CT / 2; ++h) asm volatile("" : "+v"(r.w[h]), "+v"(r.sc[h]));
+#pragma unroll
+    for (int m = 0; m < R / 16; ++m) asm volatile("" : "+v"(r.a[m]));
 }
 
-// One k step from register set r: conversion of the two column tiles'
-// nibbles, then the MFMAs of row groups m < MT.
-template <int MT>
-__device__ __forceinline__ void s_k_step_mt(const SKReg &r, int ks, f32x4 (&acc)[4][2]) {
-    bf16x8 b[2];
+// One k step from register set r: conversion of the CT column tiles'
+// nibbles, then the MFMAs of row groups m < MT; acc[t][m] is column tile t.
+template <int R, int CT, int MT>
+__device__ __forceinline__ void s_k_step_mt(const SKReg<R, CT> &r, int ks, f32x4 (&acc)[CT][R / 16]) {
+    bf16x8 b[CT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const uint32_t e = (r.sc[t] >> (8 * ks)) & 0xffu;
+    for (int t = 0; t < CT; ++t) {
+        const uint32_t e = (r.sc[t / 2][t & 1] >> (8 * ks)) & 0xffu;
         // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
-        const uint32_t q = r.w[t] & (e == 0 ? 0x88888888u : 0xffffffffu);
+        const uint32_t q = r.w[t / 2][t & 1] & (e == 0 ? 0x88888888u : 0xffffffffu);
         b[t] = dequant8(q, e8m0_to_f32(e));
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const bf16x8 a = __builtin_bit_cast(bf16x8, r.a[m]);
-        acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[0], a, acc[m][0], 0, 0, 0);
-        acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[1], a, acc[m][1], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < CT; ++t)
+            acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[t], a, acc[t][m], 0, 0, 0);
     }
 }
+
 // One stage of the prefetching consumer c with MT row groups and NKS k
 // steps.  On entry set ks & 1 holds k step ks of this stage for ks = 0, 1,
 // and rd = the LDS operations of the last set read; on exit the sets hold k
@@ -2794,17 +2822,18 @@ __device__ __forceinline__ void s_k_step_mt(const SKReg &r, int ks, f32x4 (&acc)
 // Slot j computes k step j, then reads into the same set the k step two
 // ahead in the stream: with NKS = 4 slots 0, 1 read k steps 2, 3 of this
 // stage (slots w0 / a0) and slots 2, 3 k steps 0, 1 of the next (w1 / a1).
-template <int MT, int NKS>
-__device__ __forceinline__ void s_stage_pre(SKReg (&r)[2], int &rd, bool nxt, uint32_t w0, uint32_t a0,
-                                            uint32_t w1, uint32_t a1, int c, int lane, f32x4 (&acc)[4][2]) {
+template <int R, int CT, int MT, int NKS>
+__device__ __forceinline__ void s_stage_pre(SKReg<R, CT> (&r)[2], int &rd, bool nxt, uint32_t w0,
+                                            uint32_t a0, uint32_t w1, uint32_t a1, int c, int lane,
+                                            f32x4 (&acc)[CT][R / 16]) {
 #pragma unroll
     for (int j = 0; j < NKS; ++j) {
         s_wait_set(r[j & 1], rd);
         __builtin_amdgcn_sched_barrier(0);
-        s_k_step_mt<MT>(r[j & 1], j, acc);
+        s_k_step_mt<R, CT, MT>(r[j & 1], j, acc);
         __builtin_amdgcn_sched_barrier(0);
-        if (NKS == 4 && j < 2) rd = s_read_k<false>(w0, a0, c, j + 2, MT, r[j & 1], lane);
-        else rd = s_read_k<true>(w1, a1, c, j - (NKS - 2), nxt ? MT : 0, r[j & 1], lane);
+        if (NKS == 4 && j < 2) rd = s_read_k<R, CT, false>(w0, a0, c, j + 2, MT, r[j & 1], lane);
+        else rd = s_read_k<R, CT, true>(w1, a1, c, j - (NKS - 2), nxt ? MT : 0, r[j & 1], lane);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -2812,51 +2841,66 @@ __device__ __forceinline__ void s_stage_pre(SKReg (&r)[2], int &rd, bool nxt, ui
 // The stages of one item for the prefetching consumer c with MT row groups
 // (MT = 0: the wave has no weight unit in this item and only keeps the
 // barriers): register sets and accumulators local to the item (k steps 0, 1
-// of its first stage read cold), the epilogue after the last stage.  s = the
-// stage index of the item's first stage, whose barrier has passed; on return
-// cur and s stand at the next item and its first barrier has passed.
-// Returns false when no stage is left.
-template <bool kMlp1, int MT, bool kHalf>
-__device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<64> &sh, SCursor &cur, int &s,
+// of its first stage read cold), the epilogue of each of its CT / 2 weight
+// units after the last stage.  s = the stage index of the item's first
+// stage, whose barrier has passed; on return cur and s stand at the next
+// item and its first barrier has passed.  Returns false when no stage is
+// left.
+template <bool kMlp1, int R, int CT, int MT, bool kHalf>
+__device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<R> &sh, SCursor &cur, int &s,
                                            int KP, int c) {
-    constexpr int kDW = SDepth<64>::W, kDA = SDepth<64>::A;
+    constexpr int kDW = SDepth<R>::W, kDA = SDepth<R>::A;
     const uint32_t wbase = lds_addr32(&sh.w[0]), abase = lds_addr32(&sh.a[0]);
     // the lane through an opaque move: the read addresses derived from it are
     // built inside the item, not hoisted out of the item loop for every item
     // variant at once (that alone overran the register budget)
     int lane = threadIdx.x & 63;
     asm volatile("" : "+v"(lane));
-    SKReg r[2];
+    SKReg<R, CT> r[2];
     int rd = 0;
-    f32x4 acc[4][2];
+    f32x4 acc[CT][R / 16];
     if constexpr (MT > 0) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
-        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
-        s_read_k<true>(w0, a0, c, 0, MT, r[0], lane);
-        rd = s_read_k<true>(w0, a0, c, 1, MT, r[1], lane);
+        for (int t = 0; t < CT; ++t)
+#pragma unroll
+            for (int m = 0; m < R / 16; ++m) acc[t][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
+        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
+        s_read_k<R, CT, true>(w0, a0, c, 0, MT, r[0], lane);
+        rd = s_read_k<R, CT, true>(w0, a0, c, 1, MT, r[1], lane);
     }
     // stages 0 .. KP - 2 of the item: four k steps each, the next stage's
     // first two read ahead
     for (int kp = 0; kp < KP - 1; ++kp) {
         if constexpr (MT > 0) {
-            const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
-            const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
-            const uint32_t w1 = wbase + (uint32_t)(((s + 1) % kDW) * sizeof(SWSlotR<64>));
-            const uint32_t a1 = abase + (uint32_t)(((s + 1) % kDA) * sizeof(SASlotR<64>));
-            s_stage_pre<MT, 4>(r, rd, true, w0, a0, w1, a1, c, lane, acc);
+            const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
+            const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
+            const uint32_t w1 = wbase + (uint32_t)(((s + 1) % kDW) * sizeof(SWSlotR<R>));
+            const uint32_t a1 = abase + (uint32_t)(((s + 1) % kDA) * sizeof(SASlotR<R>));
+            s_stage_pre<R, CT, MT, 4>(r, rd, true, w0, a0, w1, a1, c, lane, acc);
         }
         cur.next<true>();
         ++s;
         s_barrier_mem();
     }
-    // the last stage (64 k when kHalf: K % 128 != 0), then the epilogue
+    // the last stage (64 k when kHalf: K % 128 != 0), then the epilogues
     if constexpr (MT > 0) {
-        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<64>));
-        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<64>));
-        s_stage_pre<MT, kHalf ? 2 : 4>(r, rd, false, w0, a0, w0, a0, c, lane, acc);
-        s_epilogue<MT, kMlp1, 64, true>(a, sh.w[s % kDW], cur.tl, cur.f, c, acc);
+        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
+        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
+        s_stage_pre<R, CT, MT, kHalf ? 2 : 4>(r, rd, false, w0, a0, w0, a0, c, lane, acc);
+#pragma unroll
+        for (int h = 0; h < CT / 2; ++h) {
+            const int u = (CT / 2) * c + h;  // the item's weight unit
+            if (u < cur.cnt) {
+                f32x4 au[R / 16][2];
+#pragma unroll
+                for (int m = 0; m < R / 16; ++m) {
+                    au[m][0] = acc[2 * h][m];
+                    au[m][1] = acc[2 * h + 1][m];
+                }
+                s_epilogue<MT, kMlp1, R, true>(a, sh.w[s % kDW], cur.tl, cur.f, u, au);
+            }
+        }
     }
     cur.next<true>();
     ++s;
@@ -2866,27 +2910,50 @@ __device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<64> &sh, 
 }
 
 // The prefetching consumer c over all its items (kHalf: the last stage of
-// an item holds 64 k).
-template <bool kMlp1, bool kHalf>
-__device__ __forceinline__ void s_consume_pre(const GemmArgs &a, SSharedR<64> &sh, SCursor &cur, int KP,
+// an item holds 64 k).  One dispatch per item on its row groups (a guard
+// per row group made the compiler copy and spill the accumulators).
+template <bool kMlp1, int R, int CT, bool kHalf>
+__device__ __forceinline__ void s_consume_pre(const GemmArgs &a, SSharedR<R> &sh, SCursor &cur, int KP,
                                               int c) {
     int s = 0;
     s_barrier_mem();
     for (bool more = true; more;) {
-        const int mt = c < cur.cnt ? (cur.tl.rows + 15) >> 4 : 0;
+        const int mt = (CT / 2) * c < cur.cnt ? (cur.tl.rows + 15) >> 4 : 0;
         switch (mt) {
-            case 0: more = s_item_pre<kMlp1, 0, kHalf>(a, sh, cur, s, KP, c); break;
-            case 1: more = s_item_pre<kMlp1, 1, kHalf>(a, sh, cur, s, KP, c); break;
-            case 2: more = s_item_pre<kMlp1, 2, kHalf>(a, sh, cur, s, KP, c); break;
-            case 3: more = s_item_pre<kMlp1, 3, kHalf>(a, sh, cur, s, KP, c); break;
-            default: more = s_item_pre<kMlp1, 4, kHalf>(a, sh, cur, s, KP, c); break;
+            case 0: more = s_item_pre<kMlp1, R, CT, 0, kHalf>(a, sh, cur, s, KP, c); break;
+            case 1: more = s_item_pre<kMlp1, R, CT, 1, kHalf>(a, sh, cur, s, KP, c); break;
+            case 2: more = s_item_pre<kMlp1, R, CT, 2, kHalf>(a, sh, cur, s, KP, c); break;
+            case 3: more = s_item_pre<kMlp1, R, CT, 3, kHalf>(a, sh, cur, s, KP, c); break;
+            case 4: more = s_item_pre<kMlp1, R, CT, 4, kHalf>(a, sh, cur, s, KP, c); break;
+            default:
+                if constexpr (R == 128) {
+                    switch (mt) {
+                        case 5: more = s_item_pre<kMlp1, R, CT, 5, kHalf>(a, sh, cur, s, KP, c); break;
+                        case 6: more = s_item_pre<kMlp1, R, CT, 6, kHalf>(a, sh, cur, s, KP, c); break;
+                        case 7: more = s_item_pre<kMlp1, R, CT, 7, kHalf>(a, sh, cur, s, KP, c); break;
+                        default: more = s_item_pre<kMlp1, R, CT, 8, kHalf>(a, sh, cur, s, KP, c); break;
+                    }
+                }
+                break;
         }
     }
 }
 
-template <bool kMlp1, int R, bool kPre>
-__global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
-    static_assert(!kPre || R == 64, "the prefetching consumer holds at most 4 row groups");
+// Consumer kinds of stream_gemm_kernel: the default consumers (8 waves of
+// 2 column tiles, operands read at use), and the prefetching ones with CT
+// column tiles per wave (16 / CT consumer waves).
+template <int CK>
+struct SKind {
+    static constexpr int kCons = CK == 4 ? 4 : 8;     // consumer waves
+    static constexpr int kThreads = (kCons + 4) * 64;  // + 4 producer waves
+};
+
+// CK: 0 = the default consumers, 2 / 4 = prefetching consumers with that
+// many column tiles each.
+template <bool kMlp1, int R, int CK>
+__global__ __launch_bounds__(SKind<CK>::kThreads, 1) void stream_gemm_kernel(SArgs d) {
+    static_assert(CK == 0 || (CK == 2 && R == 64) || CK == 4, "consumer kind");
+    constexpr int kCons = SKind<CK>::kCons;
     constexpr int kDW = SDepth<R>::W, kDA = SDepth<R>::A;
     constexpr int kPR = R / 2;  // activation rows per producer
     __shared__ SSharedR<R> sh;
@@ -2903,30 +2970,28 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
     cur.init(a.tiles, base, ntx, UPT, KP, wg, Gx);
     if (!cur.valid()) return;
 
-    if (wave < kSCons) {
+    if (wave < kCons) {
         // ------------------------------------------------ consumers
-        f32x4 acc[R / 16][2];
-#pragma unroll
-        for (int m = 0; m < R / 16; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         const bool half_k = (K % kSK) != 0;  // the last stage holds 64 k
-        if constexpr (kPre) {
+        if constexpr (CK != 0) {
             // Barrier s certifies stages s and s + 1 (the producers wait one
             // stage further ahead) and slot s stays intact until barrier
             // s + 1.  The barrier that opens stage s + 1 closes stage s.
-            // One dispatch per item on its row groups (a guard per row group
-            // made the compiler copy and spill the accumulators).
-            if (half_k) s_consume_pre<kMlp1, true>(a, sh, cur, KP, wave);
-            else s_consume_pre<kMlp1, false>(a, sh, cur, KP, wave);
+            if (half_k) s_consume_pre<kMlp1, R, CK, true>(a, sh, cur, KP, wave);
+            else s_consume_pre<kMlp1, R, CK, false>(a, sh, cur, KP, wave);
             return;
         } else {
-        for (int s = 0; cur.valid(); ++s, cur.next()) {
-            s_barrier_mem();
-            const int mt = (cur.tl.rows + 15) >> 4;
-            const bool last = cur.kp == KP - 1;
-            if (wave < cur.cnt)
-                s_stage<kMlp1, R>(a, sh.w[s % kDW], sh.a[s % kDA], cur, wave, mt, last && half_k, last, acc);
-        }
-        return;
+            f32x4 acc[R / 16][2];
+#pragma unroll
+            for (int m = 0; m < R / 16; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; cur.valid(); ++s, cur.next()) {
+                s_barrier_mem();
+                const int mt = (cur.tl.rows + 15) >> 4;
+                const bool last = cur.kp == KP - 1;
+                if (wave < cur.cnt)
+                    s_stage<kMlp1, R>(a, sh.w[s % kDW], sh.a[s % kDA], cur, wave, mt, last && half_k, last, acc);
+            }
+            return;
         }
     }
 
@@ -2936,8 +3001,8 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
     // loads themselves.  Each producer counts its own loads exactly: ring
     // byte st % 8 = the loads it issued for stage st (at most depth - 1
     // stages are outstanding).
-    const bool wprod = wave < kSCons + 2;
-    const int p = wprod ? wave - kSCons : wave - kSCons - 2;  // 0 / 1
+    const bool wprod = wave < kCons + 2;
+    const int p = wprod ? wave - kCons : wave - kCons - 2;  // 0 / 1
     const int depth = wprod ? kDW : kDA;
     uint64_t ring = 0;
     int issued = 0, done = 0, is = 0;
@@ -3043,9 +3108,9 @@ __global__ __launch_bounds__(kSThreads, 1) void stream_gemm_kernel(SArgs d) {
     for (; is < depth - 1 && icur.valid(); ++is, icur.next()) issue(is, icur);
     int counted = 0;  // stages whose loads are in `done`
     for (int s = 0; s < is; ++s) {
-        // this wave's loads of stage s (and with kPre of stage s + 1, issued
+        // this wave's loads of stage s (and with prefetching consumers of stage s + 1, issued
         // since the ring is at least 3 deep) have landed
-        for (; counted <= (kPre ? s + 1 : s) && counted < is; ++counted)
+        for (; counted <= (CK != 0 ? s + 1 : s) && counted < is; ++counted)
             done += (int)((ring >> (8 * (counted & 7))) & 0xff);
         wait_vmcnt_dyn(issued - done);
         s_barrier_mem();
@@ -3341,7 +3406,8 @@ bool shape_ok(const gptoss_moe_shape *s) {
 constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SMALL_M_GEMM |
                                GPTOSS_MOE_FLAG_LARGE_M_GEMM | GPTOSS_MOE_FLAG_FP4_MFMA |
                                GPTOSS_MOE_FLAG_FP8_ACT | GPTOSS_MOE_FLAG_TILE_SWITCH |
-                               GPTOSS_MOE_FLAG_PREFILL_TILES | GPTOSS_MOE_FLAG_STAGE_PREFETCH;
+                               GPTOSS_MOE_FLAG_PREFILL_TILES | GPTOSS_MOE_FLAG_STAGE_PREFETCH |
+                               GPTOSS_MOE_FLAG_WIDE_CONSUMERS;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -3551,6 +3617,26 @@ void launch_quantize_act(const uint16_t *x, int rows, int K, int terms, const in
                            live_rows, q, qs);
 }
 
+// The streamed GEMM's variant for the flags: tile rows (PREFILL_TILES) and
+// consumer kind (WIDE_CONSUMERS: 4 waves of 4 column tiles; STAGE_PREFETCH:
+// 8 waves of 2, 64-row tiles only; else the default consumers).
+template <bool kMlp1>
+void launch_stream_gemm(const SArgs &sa, unsigned flags, int cap, hipStream_t st) {
+    const bool rows128 = stream_rows(flags) == 128;
+    if (flags & GPTOSS_MOE_FLAG_WIDE_CONSUMERS) {
+        if (rows128)
+            hipLaunchKernelGGL((stream_gemm_kernel<kMlp1, 128, 4>), dim3(cap), dim3(SKind<4>::kThreads), 0, st, sa);
+        else
+            hipLaunchKernelGGL((stream_gemm_kernel<kMlp1, 64, 4>), dim3(cap), dim3(SKind<4>::kThreads), 0, st, sa);
+    } else if (rows128) {
+        hipLaunchKernelGGL((stream_gemm_kernel<kMlp1, 128, 0>), dim3(cap), dim3(SKind<0>::kThreads), 0, st, sa);
+    } else if (flags & GPTOSS_MOE_FLAG_STAGE_PREFETCH) {
+        hipLaunchKernelGGL((stream_gemm_kernel<kMlp1, 64, 2>), dim3(cap), dim3(SKind<2>::kThreads), 0, st, sa);
+    } else {
+        hipLaunchKernelGGL((stream_gemm_kernel<kMlp1, 64, 0>), dim3(cap), dim3(SKind<0>::kThreads), 0, st, sa);
+    }
+}
+
 int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const uint16_t *x,
                    uint16_t *out, int T, unsigned flags, const WsLayout &L, const Ptrs &p,
                    hipStream_t st, Marks *mk = nullptr) {
@@ -3585,12 +3671,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
     else if (direct) {
         const SArgs sa{a1x, reinterpret_cast<const uint4 *>(w->packed + PL.w1), w->packed + PL.s1,
                        p.row_token};
-        if (stream_rows(flags) == 128)
-            hipLaunchKernelGGL((stream_gemm_kernel<true, 128, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
-        else if (flags & GPTOSS_MOE_FLAG_STAGE_PREFETCH)
-            hipLaunchKernelGGL((stream_gemm_kernel<true, 64, true>), dim3(cap), dim3(kSThreads), 0, st, sa);
-        else
-            hipLaunchKernelGGL((stream_gemm_kernel<true, 64, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
+        launch_stream_gemm<true>(sa, flags, cap, st);
         if (big < INT_MAX)  // the experts the streamed GEMM's tile list left out
             hipLaunchKernelGGL((large_m_gemm_kernel<true, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a1x,
                                p.counts, p.offsets, s->n_experts,
@@ -3625,12 +3706,7 @@ int launch_experts(const gptoss_moe_shape *s, const gptoss_moe_weights *w, const
                            p.counts, p.offsets, s->n_experts, LPacked{nullptr, nullptr, nullptr, 0});
     else if (direct) {
         const SArgs sa{a2, reinterpret_cast<const uint4 *>(w->packed + PL.w2), w->packed + PL.s2, nullptr};
-        if (stream_rows(flags) == 128)
-            hipLaunchKernelGGL((stream_gemm_kernel<false, 128, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
-        else if (flags & GPTOSS_MOE_FLAG_STAGE_PREFETCH)
-            hipLaunchKernelGGL((stream_gemm_kernel<false, 64, true>), dim3(cap), dim3(kSThreads), 0, st, sa);
-        else
-            hipLaunchKernelGGL((stream_gemm_kernel<false, 64, false>), dim3(cap), dim3(kSThreads), 0, st, sa);
+        launch_stream_gemm<false>(sa, flags, cap, st);
         if (big < INT_MAX)
             hipLaunchKernelGGL((large_m_gemm_kernel<false, true>), dim3(cap), dim3(kLWaves * 64), 0, st, a2,
                                p.counts, p.offsets, s->n_experts,

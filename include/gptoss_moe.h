@@ -86,6 +86,14 @@ extern "C" {
  * bit-identical to the default.  Ignored with PREFILL_TILES and on the other
  * GEMM paths.  No counterpart in the reference (a schedule, not a result). */
 #define GPTOSS_MOE_FLAG_STAGE_PREFETCH 128u
+/* Wide prefetching consumers on the streamed GEMM (packed weights): 4
+ * consumer waves of 4 column tiles each instead of 8 of 2, reading operands
+ * ahead as STAGE_PREFETCH does; each activation fragment read from LDS feeds
+ * four MFMAs instead of two, which halves the LDS reads per MFMA.  With
+ * PREFILL_TILES on 128-row tiles, else on 64-row tiles.  Same MFMAs in the
+ * same k order per output: bit-identical to the default.  No counterpart in
+ * the reference (a schedule, not a result). */
+#define GPTOSS_MOE_FLAG_WIDE_CONSUMERS 256u
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {

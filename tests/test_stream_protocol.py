@@ -77,7 +77,7 @@ class LdsQueue:
         return self.ops - self.last_of[tag] >= n
 
 
-def consumer_pre(stages, KP, half, c, always_two=False):
+def consumer_pre(stages, KP, half, c, always_two=False, CT=2):
     """The prefetching consumer c: a list of (phase, stage) reads with the
     phase their data is used in (returned by then), and the k steps it
     computes; asserts set contents and lgkmcnt coverage on the way."""
@@ -93,7 +93,7 @@ def consumer_pre(stages, KP, half, c, always_two=False):
 
     def read_k(stage, ks, mt, p, ph):
         with_sc = ks < 2  # s_read_k<kSc>: only k steps 0, 1 read the e8m0 words
-        n = 1 + with_sc + mt if mt > 0 else 0
+        n = (CT // 2) * (1 + with_sc) + mt if mt > 0 else 0
         if n:
             sets[p] = (stage, ks)
             if with_sc:
@@ -105,14 +105,14 @@ def consumer_pre(stages, KP, half, c, always_two=False):
     def use_set(p, stage, ks, rd_, ph):
         assert sets[p] == (stage, ks), (sets[p], stage, ks)
         assert sc_of[p] == stage, (sc_of[p], stage)
-        n = 2 if (rd_ > 0 or always_two) else 0
+        n = CT // 2 + 1 if (rd_ > 0 or always_two) else 0  # s_min_ops
         assert q.wait_covers((stage, ks, p), n)
         computed.append((stage, ks, ph))
 
     while True:
         item, kp0, cnt, mt_rows = stages[s]
         assert kp0 == 0
-        mt = mt_rows if c < cnt else 0
+        mt = mt_rows if (CT // 2) * c < cnt else 0
         if mt > 0:
             read_k(s, 0, mt, 0, phase)
             rd = read_k(s, 1, mt, 1, phase)
@@ -167,24 +167,32 @@ def check_ring(stages, reads_with_use, issue, landed, depth, pre):
             assert issue[nxt] > u, (t, r, u, issue[nxt])
 
 
-def random_items(rng, KP):
+def random_items(rng, KP, R=64):
     n = rng.randint(1, 6)
-    return [(rng.randint(1, 64), rng.randint(1, 8)) for _ in range(n)]
+    return [(rng.randint(1, R), rng.randint(1, 8)) for _ in range(n)]
 
 
-@pytest.mark.parametrize("seed", range(40))
-@pytest.mark.parametrize("pre", [False, True])
-def test_ring_protocol(seed, pre):
-    rng = random.Random(seed * 2 + pre)
+# (consumer kind, tile rows): the default consumers and the prefetching ones
+# with 2 or 4 column tiles per wave; rings 5 / 4 deep for 64-row tiles, 3 / 3
+# for 128-row tiles (SDepth)
+KINDS = [(0, 64), (0, 128), (2, 64), (4, 64), (4, 128)]
+
+
+@pytest.mark.parametrize("seed", range(30))
+@pytest.mark.parametrize("kind,R", KINDS)
+def test_ring_protocol(seed, kind, R):
+    pre = kind != 0
+    CT = kind or 2
+    rng = random.Random(seed * 7 + kind + R)
     KP = rng.choice([1, 2, 3, 23])
     half = rng.random() < 0.5 and KP > 0
-    items = random_items(rng, KP)
+    items = random_items(rng, KP, R)
     stages = stages_of(items, KP)
-    for depth in (5, 4):
+    for depth in ((5, 4) if R == 64 else (3,)):
         issue, landed = producer_schedule(len(stages), depth, pre)
-        for c in range(8):
+        for c in range(16 // CT):
             if pre:
-                reads, _ = consumer_pre(stages, KP, half, c)
+                reads, _ = consumer_pre(stages, KP, half, c, CT=CT)
                 # a read is used by the end of the phase after it at the latest
                 # (k steps 0, 1 of the next stage), else in its own phase
                 with_use = []
@@ -197,17 +205,19 @@ def test_ring_protocol(seed, pre):
 
 
 @pytest.mark.parametrize("seed", range(20))
-def test_prefetch_computes_every_k_step_once(seed):
+@pytest.mark.parametrize("CT,R", [(2, 64), (4, 64), (4, 128)])
+def test_prefetch_computes_every_k_step_once(seed, CT, R):
     rng = random.Random(1000 + seed)
     KP = rng.choice([1, 2, 5, 23])
     half = rng.random() < 0.5
-    items = random_items(rng, KP)
+    items = random_items(rng, KP, R)
     stages = stages_of(items, KP)
-    for c in range(8):
-        _, computed = consumer_pre(stages, KP, half, c)
+    units = [0] * 8
+    for c in range(16 // CT):
+        _, computed = consumer_pre(stages, KP, half, c, CT=CT)
         want = []
         for s, (_, kp, cnt, _) in enumerate(stages):
-            if c < cnt:
+            if (CT // 2) * c < cnt:
                 nks = 2 if (half and kp == KP - 1) else 4
                 want += [(s, j) for j in range(nks)]
         assert [(s, j) for s, j, _ in computed] == want
@@ -247,3 +257,17 @@ def test_model_flags_lgkmcnt2_without_a_later_set():
     consumer_pre(stages, 3, False, 0)
     with pytest.raises(AssertionError):
         consumer_pre(stages, 3, False, 0, always_two=True)
+
+
+@pytest.mark.parametrize("CT", [2, 4])
+def test_every_weight_unit_has_one_consumer(CT):
+    """Consumer c owns weight units (CT / 2) c .. (CT / 2) c + CT / 2 - 1 of an
+    item (the epilogue skips units >= cnt): each of the item's units once."""
+    for cnt in range(1, 9):
+        owned = []
+        for c in range(16 // CT):
+            for h in range(CT // 2):
+                u = (CT // 2) * c + h
+                if u < cnt:
+                    owned.append(u)
+        assert sorted(owned) == list(range(cnt))
