@@ -2678,6 +2678,22 @@ __device__ __forceinline__ void s_stage(const GemmArgs &a, const SWSlotR<R> &ws,
     }
 }
 
+// Consumer kinds of stream_gemm_kernel: the default consumers (8 waves of
+// 2 column tiles, operands read at use), and the prefetching ones with CT
+// column tiles per wave (16 / CT consumer waves).
+// The prefetching consumers read a stage's first two k steps during the
+// previous stage (cross) on 64-row tiles, whose rings (5 and 4 deep) leave
+// the producers two stages of lookahead when they wait one stage earlier;
+// on 128-row tiles (3-deep rings) they read them at the stage's start and
+// the producers keep the default wait.
+template <int CK>
+struct SKind {
+    static constexpr int kCons = CK == 4 ? 4 : 8;     // consumer waves
+    static constexpr int kThreads = (kCons + 4) * 64;  // + 4 producer waves
+    template <int R>
+    static constexpr bool cross() { return CK != 0 && R == 64; }
+};
+
 // The prefetching consumers (GPTOSS_MOE_FLAG_STAGE_PREFETCH: 8 waves of
 // CT = 2 column tiles on 64-row tiles; GPTOSS_MOE_FLAG_WIDE_CONSUMERS: 4
 // waves of CT = 4 column tiles, on 64- or 128-row tiles).  The k steps of a
@@ -2850,6 +2866,7 @@ template <bool kMlp1, int R, int CT, int MT, bool kHalf>
 __device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<R> &sh, SCursor &cur, int &s,
                                            int KP, int c) {
     constexpr int kDW = SDepth<R>::W, kDA = SDepth<R>::A;
+    constexpr bool kCross = SKind<CT>::template cross<R>();
     const uint32_t wbase = lds_addr32(&sh.w[0]), abase = lds_addr32(&sh.a[0]);
     // the lane through an opaque move: the read addresses derived from it are
     // built inside the item, not hoisted out of the item loop for every item
@@ -2859,25 +2876,31 @@ __device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<R> &sh, S
     SKReg<R, CT> r[2];
     int rd = 0;
     f32x4 acc[CT][R / 16];
+    // k steps 0, 1 of stage s (the item's first stage; every stage without
+    // kCross)
+    auto cold = [&]() {
+        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
+        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
+        s_read_k<R, CT, true>(w0, a0, c, 0, MT, r[0], lane);
+        rd = s_read_k<R, CT, true>(w0, a0, c, 1, MT, r[1], lane);
+    };
     if constexpr (MT > 0) {
 #pragma unroll
         for (int t = 0; t < CT; ++t)
 #pragma unroll
             for (int m = 0; m < R / 16; ++m) acc[t][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
-        const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
-        s_read_k<R, CT, true>(w0, a0, c, 0, MT, r[0], lane);
-        rd = s_read_k<R, CT, true>(w0, a0, c, 1, MT, r[1], lane);
+        if constexpr (kCross) cold();
     }
     // stages 0 .. KP - 2 of the item: four k steps each, the next stage's
-    // first two read ahead
+    // first two read ahead with kCross
     for (int kp = 0; kp < KP - 1; ++kp) {
         if constexpr (MT > 0) {
+            if constexpr (!kCross) cold();
             const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
             const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
             const uint32_t w1 = wbase + (uint32_t)(((s + 1) % kDW) * sizeof(SWSlotR<R>));
             const uint32_t a1 = abase + (uint32_t)(((s + 1) % kDA) * sizeof(SASlotR<R>));
-            s_stage_pre<R, CT, MT, 4>(r, rd, true, w0, a0, w1, a1, c, lane, acc);
+            s_stage_pre<R, CT, MT, 4>(r, rd, kCross, w0, a0, w1, a1, c, lane, acc);
         }
         cur.next<true>();
         ++s;
@@ -2885,6 +2908,7 @@ __device__ __forceinline__ bool s_item_pre(const GemmArgs &a, SSharedR<R> &sh, S
     }
     // the last stage (64 k when kHalf: K % 128 != 0), then the epilogues
     if constexpr (MT > 0) {
+        if constexpr (!kCross) cold();
         const uint32_t w0 = wbase + (uint32_t)((s % kDW) * sizeof(SWSlotR<R>));
         const uint32_t a0 = abase + (uint32_t)((s % kDA) * sizeof(SASlotR<R>));
         s_stage_pre<R, CT, MT, kHalf ? 2 : 4>(r, rd, false, w0, a0, w0, a0, c, lane, acc);
@@ -2939,14 +2963,6 @@ __device__ __forceinline__ void s_consume_pre(const GemmArgs &a, SSharedR<R> &sh
     }
 }
 
-// Consumer kinds of stream_gemm_kernel: the default consumers (8 waves of
-// 2 column tiles, operands read at use), and the prefetching ones with CT
-// column tiles per wave (16 / CT consumer waves).
-template <int CK>
-struct SKind {
-    static constexpr int kCons = CK == 4 ? 4 : 8;     // consumer waves
-    static constexpr int kThreads = (kCons + 4) * 64;  // + 4 producer waves
-};
 
 // CK: 0 = the default consumers, 2 / 4 = prefetching consumers with that
 // many column tiles each.
@@ -2974,9 +2990,10 @@ __global__ __launch_bounds__(SKind<CK>::kThreads, 1) void stream_gemm_kernel(SAr
         // ------------------------------------------------ consumers
         const bool half_k = (K % kSK) != 0;  // the last stage holds 64 k
         if constexpr (CK != 0) {
-            // Barrier s certifies stages s and s + 1 (the producers wait one
-            // stage further ahead) and slot s stays intact until barrier
-            // s + 1.  The barrier that opens stage s + 1 closes stage s.
+            // Barrier s certifies stage s (and stage s + 1 on 64-row tiles,
+            // where the producers wait one stage further ahead), and slot s
+            // stays intact until barrier s + 1.  The barrier that opens stage
+            // s + 1 closes stage s.
             if (half_k) s_consume_pre<kMlp1, R, CK, true>(a, sh, cur, KP, wave);
             else s_consume_pre<kMlp1, R, CK, false>(a, sh, cur, KP, wave);
             return;
@@ -3110,7 +3127,7 @@ __global__ __launch_bounds__(SKind<CK>::kThreads, 1) void stream_gemm_kernel(SAr
     for (int s = 0; s < is; ++s) {
         // this wave's loads of stage s (and with prefetching consumers of stage s + 1, issued
         // since the ring is at least 3 deep) have landed
-        for (; counted <= (CK != 0 ? s + 1 : s) && counted < is; ++counted)
+        for (; counted <= (SKind<CK>::template cross<R>() ? s + 1 : s) && counted < is; ++counted)
             done += (int)((ring >> (8 * (counted & 7))) & 0xff);
         wait_vmcnt_dyn(issued - done);
         s_barrier_mem();

@@ -77,7 +77,7 @@ class LdsQueue:
         return self.ops - self.last_of[tag] >= n
 
 
-def consumer_pre(stages, KP, half, c, always_two=False, CT=2):
+def consumer_pre(stages, KP, half, c, always_two=False, CT=2, cross=True):
     """The prefetching consumer c: a list of (phase, stage) reads with the
     phase their data is used in (returned by then), and the k steps it
     computes; asserts set contents and lgkmcnt coverage on the way."""
@@ -116,20 +116,27 @@ def consumer_pre(stages, KP, half, c, always_two=False, CT=2):
         if mt > 0:
             read_k(s, 0, mt, 0, phase)
             rd = read_k(s, 1, mt, 1, phase)
-        # stages 0 .. KP - 2
+        # stages 0 .. KP - 2 (without cross: k steps 0, 1 read at each stage's
+        # start, the next stage's not read ahead)
         for kp in range(KP - 1):
             if mt > 0:
+                if not cross and kp > 0:
+                    read_k(s, 0, mt, 0, phase)
+                    rd = read_k(s, 1, mt, 1, phase)
                 for j in range(4):
                     use_set(j & 1, s, j, rd, phase)
                     if j < 2:
                         rd = read_k(s, j + 2, mt, j & 1, phase)
                     else:
-                        rd = read_k(s + 1, j - 2, mt, j & 1, phase)
+                        rd = read_k(s + 1, j - 2, mt if cross else 0, j & 1, phase)
             s += 1
             phase += 1  # barrier
         # last stage
         nks = 2 if half else 4
         if mt > 0:
+            if not cross and KP > 1:
+                read_k(s, 0, mt, 0, phase)
+                rd = read_k(s, 1, mt, 1, phase)
             for j in range(nks):
                 use_set(j & 1, s, j, rd, phase)
                 if nks == 4 and j < 2:
@@ -188,11 +195,12 @@ def test_ring_protocol(seed, kind, R):
     half = rng.random() < 0.5 and KP > 0
     items = random_items(rng, KP, R)
     stages = stages_of(items, KP)
+    cross = pre and R == 64  # SKind::cross: read ahead across stages on 64-row tiles only
     for depth in ((5, 4) if R == 64 else (3,)):
-        issue, landed = producer_schedule(len(stages), depth, pre)
+        issue, landed = producer_schedule(len(stages), depth, cross)
         for c in range(16 // CT):
             if pre:
-                reads, _ = consumer_pre(stages, KP, half, c, CT=CT)
+                reads, _ = consumer_pre(stages, KP, half, c, CT=CT, cross=cross)
                 # a read is used by the end of the phase after it at the latest
                 # (k steps 0, 1 of the next stage), else in its own phase
                 with_use = []
@@ -214,7 +222,7 @@ def test_prefetch_computes_every_k_step_once(seed, CT, R):
     stages = stages_of(items, KP)
     units = [0] * 8
     for c in range(16 // CT):
-        _, computed = consumer_pre(stages, KP, half, c, CT=CT)
+        _, computed = consumer_pre(stages, KP, half, c, CT=CT, cross=R == 64)
         want = []
         for s, (_, kp, cnt, _) in enumerate(stages):
             if (CT // 2) * c < cnt:
@@ -271,3 +279,16 @@ def test_every_weight_unit_has_one_consumer(CT):
                 if u < cnt:
                     owned.append(u)
         assert sorted(owned) == list(range(cnt))
+
+
+def test_model_flags_a_one_stage_lookahead_on_3_deep_rings():
+    # reading ahead across stages (producers waiting one stage earlier) on
+    # a 3-deep ring would still be correct, but leaves the producers only one
+    # stage of lookahead; the kernel does not do it (SKind::cross), and the
+    # model of the kernel's choice keeps two: issue of stage t at least two
+    # barriers before the barrier that certifies it
+    stages = stages_of([(100, 8), (60, 5)], 6)
+    issue, landed = producer_schedule(len(stages), 3, False)
+    assert all(landed[t] - issue[t] >= 1 for t in range(3, len(stages)))
+    issue, landed = producer_schedule(len(stages), 3, True)
+    assert any(landed[t] - issue[t] < 1 for t in range(3, len(stages)))
