@@ -52,6 +52,10 @@ def parse():
     ap.add_argument("--new-variants", action="store_true",
                     help="also the prefetching-consumer, 128-row-tile and tile-switch variant lines (kernels whose GPU "
                          "tests have not passed yet)")
+    ap.add_argument("--path", default="auto",
+                    help="GEMM path of the timed line (gptoss_moe path names: auto, prefetch, wide, "
+                         "wide_prefill, prefill, switch, ...); anything but auto is a variant "
+                         "measurement, recorded in config.gemm_path (for profiling a variant)")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the extra block-scaled FP4 MFMA variant lines")
     ap.add_argument("--profile-iters", type=int, default=20)
@@ -506,8 +510,9 @@ def main():
     fw = None if d.forced_w is None else torch.from_numpy(d.forced_w.view(np.int16)).to(dev)
     out = torch.empty_like(x)
 
+    P = args.path
     for i in range(args.warmup):
-        layers[i % copies].forward(x, out, fi, fw)
+        layers[i % copies].forward(x, out, fi, fw, path=P)
     torch.cuda.synchronize()
     # one event between consecutive steps (same stream): per-step times for
     # the median and p90; the headline is the total over the K steps
@@ -515,7 +520,7 @@ def main():
     t0 = time.perf_counter()
     evs[0].record()
     for i in range(args.steps):
-        layers[i % copies].forward(x, out, fi, fw)
+        layers[i % copies].forward(x, out, fi, fw, path=P)
         evs[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -527,7 +532,7 @@ def main():
     # per-kernel durations (HIP events between kernels on the launch stream)
     prof = {k: [] for k in gptoss_moe.MoeLayer.KERNELS}
     for i in range(args.profile_iters):
-        r = layers[i % copies].forward_profiled(x, out, fi, fw)
+        r = layers[i % copies].forward_profiled(x, out, fi, fw, path=P)
         for k, v in r.items():
             prof[k].append(v)
     kms = {k: statistics.median(v) for k, v in prof.items()}
@@ -578,7 +583,7 @@ def main():
         "data": "synthetic (seeded random MXFP4 weights, bf16 activations)",
         "config": {"workload": c.name, "hidden": H, "intermediate": D, "n_experts": c.n_experts,
                    "top_k": c.top_k, "tokens": c.tokens, "routing": c.routing,
-                   "weight_copies_rotated": copies},
+                   "weight_copies_rotated": copies, **({"gemm_path": P} if P != "auto" else {})},
         "roofline": roofline,
         "layer": {"algorithmic_bytes": alg_bytes, "hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
                   "hbm_frac": round(alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
