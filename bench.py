@@ -437,12 +437,16 @@ def time_variants(layers, x, out, fi, fw, args, c, flops):
     flags = {"prefill": "GPTOSS_MOE_FLAG_PREFILL_TILES", "switch": "GPTOSS_MOE_FLAG_TILE_SWITCH",
              "prefetch": "GPTOSS_MOE_FLAG_STAGE_PREFETCH", "wide": "GPTOSS_MOE_FLAG_WIDE_CONSUMERS",
              "wide_prefill": "GPTOSS_MOE_FLAG_WIDE_CONSUMERS | GPTOSS_MOE_FLAG_PREFILL_TILES",
+             "wpf": "GPTOSS_MOE_FLAG_WEIGHT_PREFETCH",
+             "wide_wpf": "GPTOSS_MOE_FLAG_WIDE_CONSUMERS | GPTOSS_MOE_FLAG_WEIGHT_PREFETCH",
              "fp4": "GPTOSS_MOE_FLAG_FP4_MFMA", "fp4_fp8": "GPTOSS_MOE_FLAG_FP4_MFMA | GPTOSS_MOE_FLAG_FP8_ACT"}
     paths = [("fp4", "MXFP8 activations, hi + lo terms"), ("fp4_fp8", "MXFP8 activations, hi term only")]
     if getattr(args, "new_variants", False):
         paths = [("prefetch", "bf16, prefetching consumers on the streamed GEMM"),
                  ("wide", "bf16, wide prefetching consumers (4 column tiles per wave), 64-row tiles"),
                  ("wide_prefill", "bf16, wide prefetching consumers, 128-row tiles"),
+                 ("wpf", "bf16, MLP1 weights prefetched into the memory-side cache during routing"),
+                 ("wide_wpf", "bf16, wide consumers + MLP1 weight prefetch"),
                  ("prefill", "bf16, 128-row tiles on the streamed GEMM"),
                  ("switch", "bf16, experts of 128+ rows on the large-M GEMM")] + paths
     for path, note in paths:

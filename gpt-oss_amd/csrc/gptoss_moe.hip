@@ -3424,7 +3424,7 @@ constexpr unsigned kFlagsAll = GPTOSS_MOE_FLAG_RESIDUAL_ADD | GPTOSS_MOE_FLAG_SM
                                GPTOSS_MOE_FLAG_LARGE_M_GEMM | GPTOSS_MOE_FLAG_FP4_MFMA |
                                GPTOSS_MOE_FLAG_FP8_ACT | GPTOSS_MOE_FLAG_TILE_SWITCH |
                                GPTOSS_MOE_FLAG_PREFILL_TILES | GPTOSS_MOE_FLAG_STAGE_PREFETCH |
-                               GPTOSS_MOE_FLAG_WIDE_CONSUMERS;
+                               GPTOSS_MOE_FLAG_WIDE_CONSUMERS | GPTOSS_MOE_FLAG_WEIGHT_PREFETCH;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -3632,6 +3632,78 @@ void launch_quantize_act(const uint16_t *x, int rows, int K, int terms, const in
     if (grid > 0)
         hipLaunchKernelGGL(quantize_act_kernel, dim3(grid), dim3(256), 0, st, x, rows, K, terms,
                            live_rows, q, qs);
+}
+
+// Weight prefetch (GPTOSS_MOE_FLAG_WEIGHT_PREFETCH): reads the first S
+// k stages of every expert's packed MLP1 nibbles (column tile j of expert e:
+// bytes ((e CT + j) KP + kp) KB, kp < S) and their e8m0 blocks ((e KP + kp)
+// CT 64 bytes, kp < S), so that they sit in the memory-side cache when the
+// streamed GEMM asks for them.  Read-only: the values only feed a register
+// the compiler must keep, nothing is written.
+__global__ __launch_bounds__(256) void weight_prefetch_kernel(const uint4 *__restrict__ w,
+                                                              const uint4 *__restrict__ sc, int E, int CT,
+                                                              int KP, int S) {
+    const size_t per_w = (size_t)S * 64;           // uint4 per (expert, tile) range
+    const size_t n_w = (size_t)E * CT * per_w;
+    const size_t per_s = (size_t)S * CT * 4;       // uint4 per expert's scale range
+    const size_t n_s = (size_t)E * per_s;
+    const size_t stride = (size_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_w + n_s; i += stride) {
+        const uint4 *p;
+        if (i < n_w) {
+            const size_t r = i / per_w, o = i - r * per_w;
+            p = w + r * (size_t)KP * 64 + o;
+        } else {
+            const size_t j = i - n_w, e = j / per_s, o = j - e * per_s;
+            p = sc + e * (size_t)KP * CT * 4 + o;
+        }
+        const uint4 v = *p;
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    asm volatile("" : : "v"(acc));  // the loads stay
+}
+
+// A side stream per device for the weight prefetch: created on first use,
+// kept until the process ends, default priority, non-blocking towards the
+// legacy stream.
+int prefetch_stream(hipStream_t *out) {
+    static std::mutex mu;
+    static hipStream_t streams[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= 64) return GPTOSS_MOE_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(mu);
+    if (streams[dev] == nullptr) {
+        e = hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            streams[dev] = nullptr;
+            return hip_status(e);
+        }
+    }
+    *out = streams[dev];
+    return GPTOSS_MOE_OK;
+}
+
+// Launch the prefetch of MLP1's first stages on the side stream, sized to
+// about kPrefetchBytes (what HBM streams while routing runs), at least one
+// stage.  No dependency either way: the weights are constant during a call.
+constexpr size_t kPrefetchBytes = (size_t)72 << 20;
+int launch_weight_prefetch(const gptoss_moe_shape *s, const gptoss_moe_weights *w) {
+    const PackLayout PL = pack_layout(*s);
+    const int N = 2 * s->intermediate, K = s->hidden;
+    const int CT = N / 16, KP = (K + kSK - 1) / kSK, E = s->n_experts;
+    const size_t per_stage = (size_t)E * CT * 1024 + (size_t)E * CT * 64;
+    int S = (int)(kPrefetchBytes / per_stage);
+    S = S < 1 ? 1 : (S > KP ? KP : S);
+    hipStream_t ps;
+    const int rc = prefetch_stream(&ps);
+    if (rc) return rc;
+    hipLaunchKernelGGL(weight_prefetch_kernel, dim3(4 * device_cus()), dim3(256), 0, ps,
+                       reinterpret_cast<const uint4 *>(w->packed + PL.w1),
+                       reinterpret_cast<const uint4 *>(w->packed + PL.s1), E, CT, KP, S);
+    return hip_status(hipGetLastError());
 }
 
 // The streamed GEMM's variant for the flags: tile rows (PREFILL_TILES) and
@@ -3873,6 +3945,9 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
     if (!x_norm || !out || !aligned16(x_norm) || !aligned16(out)) return GPTOSS_MOE_ERR_INVALID_ARG;
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
+    if ((flags & GPTOSS_MOE_FLAG_WEIGHT_PREFETCH) && gemm_path(shape, w, n_tokens, flags) == PATH_DIRECT &&
+        (rc = launch_weight_prefetch(shape, w)) != 0)
+        return rc;
     rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
                       gemm_tile_rows(shape, w, n_tokens, flags), switch_rows(shape, w, n_tokens, flags),
                       gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT);
@@ -3917,10 +3992,13 @@ int gptoss_moe_forward_profiled(const gptoss_moe_shape *shape, const gptoss_moe_
         }
     const WsLayout L = ws_layout(*shape, max_tokens);
     const Ptrs p = ws_ptrs(L, workspace);
+    if ((flags & GPTOSS_MOE_FLAG_WEIGHT_PREFETCH) && gemm_path(shape, w, n_tokens, flags) == PATH_DIRECT)
+        rc = launch_weight_prefetch(shape, w);
     mk.mark(stream);
-    rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
-                      gemm_tile_rows(shape, w, n_tokens, flags), switch_rows(shape, w, n_tokens, flags),
-                      gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT, &mk);
+    if (!rc)
+        rc = launch_route(shape, w, x_norm, n_tokens, forced_topk_i, forced_topk_w, p, stream,
+                          gemm_tile_rows(shape, w, n_tokens, flags), switch_rows(shape, w, n_tokens, flags),
+                          gemm_path(shape, w, n_tokens, flags) < PATH_DIRECT, &mk);
     if (!rc) rc = launch_experts(shape, w, x_norm, out, n_tokens, flags, L, p, stream, &mk);
     if (!rc) rc = hip_status(hipEventSynchronize(mk.ev[5]));
     for (int i = 0; i < 5 && !rc; ++i)

@@ -34,6 +34,7 @@ FLAG_TILE_SWITCH = 32
 FLAG_PREFILL_TILES = 64
 FLAG_STAGE_PREFETCH = 128
 FLAG_WIDE_CONSUMERS = 256
+FLAG_WEIGHT_PREFETCH = 512
 # "fp4": block-scaled FP4 MFMA on MXFP8 activations (hi + lo terms); "fp4_fp8":
 # the same with the hi term only.  Both need the packed_fp4 weights (pack_fp4()).
 # "switch": the packed path with the per-expert tile switch (experts of >= 128
@@ -42,7 +43,8 @@ _PATH_FLAGS = {"auto": 0, "small": FLAG_SMALL_M_GEMM, "large": FLAG_LARGE_M_GEMM
                "fp4": FLAG_FP4_MFMA, "fp4_fp8": FLAG_FP4_MFMA | FLAG_FP8_ACT,
                "switch": FLAG_TILE_SWITCH, "prefill": FLAG_PREFILL_TILES,
                "prefetch": FLAG_STAGE_PREFETCH, "wide": FLAG_WIDE_CONSUMERS,
-               "wide_prefill": FLAG_WIDE_CONSUMERS | FLAG_PREFILL_TILES}
+               "wide_prefill": FLAG_WIDE_CONSUMERS | FLAG_PREFILL_TILES,
+               "wpf": FLAG_WEIGHT_PREFETCH, "wide_wpf": FLAG_WIDE_CONSUMERS | FLAG_WEIGHT_PREFETCH}
 
 _ERRNAMES = {ERR_INVALID_ARG: "invalid argument", ERR_WORKSPACE: "workspace too small",
              ERR_HIP: "HIP error", ERR_UNSUPPORTED: "unsupported shape"}
@@ -366,7 +368,8 @@ class MoeLayer:
         "switch" for the per-expert tile switch on packed weights, "prefill"
         for 128-row tiles on the streamed GEMM, "prefetch" for its prefetching
         consumers, "wide" / "wide_prefill" for its wide prefetching consumers on
-        64- / 128-row tiles, or "fp4" / "fp4_fp8" for the block-scaled FP4 MFMA variant."""
+        64- / 128-row tiles, "wpf" / "wide_wpf" with the MLP1 weight prefetch
+        during routing, or "fp4" / "fp4_fp8" for the block-scaled FP4 MFMA variant."""
         import torch
         T = x_norm.shape[0]
         if out is None:

@@ -94,6 +94,14 @@ extern "C" {
  * same k order per output: bit-identical to the default.  No counterpart in
  * the reference (a schedule, not a result). */
 #define GPTOSS_MOE_FLAG_WIDE_CONSUMERS 256u
+/* Weight prefetch on gptoss_moe_forward (packed weights, streamed GEMM): a
+ * read-only kernel on a library-owned side stream (one per device, created
+ * on first use) reads the first k stages of every expert's MLP1 weights
+ * (about 72 MB) while routing runs, so that the memory-side cache holds them
+ * when the GEMM starts.  No dependency between the streams; results are
+ * unchanged.  Not for calls under HIP graph capture (the side stream is not
+ * captured).  No counterpart in the reference. */
+#define GPTOSS_MOE_FLAG_WEIGHT_PREFETCH 512u
 
 /* Shape of one MoE layer (run.cpp:25-45 Config fields). */
 typedef struct gptoss_moe_shape {

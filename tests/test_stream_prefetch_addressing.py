@@ -101,3 +101,25 @@ def test_offsets_match_the_kernel_source():
     assert "(CT * c * 64 + lane) * 16 + 4 * ks" in body
     assert "4u * (uint32_t)((CT * c) * 16 + n)" in body
     assert "(n * 256 + ((4 * ks + g) ^ n) * 16)" in body
+
+
+@pytest.mark.parametrize("H,D,E", [(2880, 2880, 32), (2880, 2880, 128), (128, 128, 4), (192, 448, 5),
+                                   (384, 320, 6)])
+def test_weight_prefetch_reads_stay_in_the_packed_copy(H, D, E):
+    """weight_prefetch_kernel: the last uint4 it reads of the nibbles and of
+    the e8m0 blocks lies inside MLP1's packed regions (pk_w_expert /
+    pk_s_expert bytes per expert), whatever S in 1 .. KP."""
+    N, K = 2 * D, H
+    CT, KP = N // 16, -(-K // 128)
+    w_bytes = E * N * KP * 64                  # pk_w_expert(N, K) per expert
+    s_bytes = E * N * (-(-K // 512)) * 16      # pk_s_expert(N, K) per expert
+    for S in {1, KP // 2 or 1, KP}:
+        per_w, per_s = S * 64, S * CT * 4
+        last_w = (E * CT - 1) * KP * 64 + per_w - 1
+        last_s = (E - 1) * KP * CT * 4 + per_s - 1
+        assert 16 * (last_w + 1) <= w_bytes
+        assert 16 * (last_s + 1) <= s_bytes
+        # and the ranges are what the GEMM's producers read first: tile j of
+        # expert e, stages kp < S
+        e, j = E - 1, CT - 1
+        assert ((e * CT + j) * KP + 0) * 64 == (e * CT + j) * KP * 64

@@ -19,7 +19,7 @@ from wip_gpu_tile_switch import _run
 pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("gpu")]
 
 
-@pytest.mark.parametrize("path", ["prefetch", "wide", "wide_prefill"])
+@pytest.mark.parametrize("path", ["prefetch", "wide", "wide_prefill", "wpf", "wide_wpf"])
 @pytest.mark.parametrize("name", ["c0_tiny", "t_odd_n", "t_large_m", "c1_20b_decode", "c2_20b_zipf",
                                   "c3a_120b_decode"])
 def test_prefetch_bit_identical(name, path):
