@@ -79,7 +79,7 @@ def test_argument_errors_without_gpu():
                                 64, 8, None) == gm.ERR_WORKSPACE
     # unknown flag bits; the FP4 variant's flags without its weights or combined wrongly
     need = gm.workspace_size(s, 8)
-    for flags in (128, gm.FLAG_FP4_MFMA, gm.FLAG_FP8_ACT,
+    for flags in (1024, 1 << 31, gm.FLAG_FP4_MFMA, gm.FLAG_FP8_ACT,
                   gm.FLAG_FP4_MFMA | gm.FLAG_SMALL_M_GEMM):
         assert lib.gptoss_moe_forward(ctypes.byref(s), ctypes.byref(w), None, None, 4, None, None,
                                       flags, fake, need, 8, None) == gm.ERR_INVALID_ARG, flags
@@ -139,9 +139,14 @@ def test_packed_weights_make_w1_w2_optional():
     s = gm.make_shape(2880, 2880, 32, 4)
     p = 1 << 20  # aligned stand-in device addresses
     base = dict(router_w=p, router_b=p, b1=p, b2=p)
-    # packed copy only: the streamed GEMM needs nothing else
+    # packed copy only: the streamed GEMM needs nothing else, with any of its
+    # opt-in variants
     w = gm.Weights(**base, packed=p)
     assert _fake_call(lib, s, w) == gm.OK
+    for flags in (gm.FLAG_PREFILL_TILES, gm.FLAG_STAGE_PREFETCH, gm.FLAG_WIDE_CONSUMERS,
+                  gm.FLAG_WIDE_CONSUMERS | gm.FLAG_PREFILL_TILES, gm.FLAG_WEIGHT_PREFETCH,
+                  gm.FLAG_WIDE_CONSUMERS | gm.FLAG_WEIGHT_PREFETCH | gm.FLAG_RESIDUAL_ADD):
+        assert _fake_call(lib, s, w, flags) == gm.OK, flags
     # no packed copy and no w1/w2: nothing to run on
     w = gm.Weights(**base)
     assert _fake_call(lib, s, w) == gm.ERR_INVALID_ARG
