@@ -1717,8 +1717,13 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t *__restrict__ w
             const int byte = fmt == 0 ? 64 * kp + 16 * q + 4 * (lane >> 4)
                                       : 64 * kp + 16 * (lane >> 4) + 4 * q;
             uint32_t v = 0;
-            if (byte < K / 2)
+            if (byte < K / 2) {
                 v = *reinterpret_cast<const uint32_t *>(wq + ((size_t)e * N + row) * (K / 2) + byte);
+                // the dword's 8 elements share 32-k group byte / 16; a zero
+                // e8m0 byte makes them +-0 (code * 0.0 in the reference), so
+                // keep only their sign bits: the GEMMs then need no fix-up
+                if (ws[((size_t)e * N + row) * KS + (byte >> 4)] == 0) v &= 0x88888888u;
+            }
             pw[i] = v;
         } else if (fmt == 0) {
             // [e][kp][ct][16 rows][4 B]: byte i of row n = group 4 kp + i;
@@ -2524,10 +2529,9 @@ __device__ __forceinline__ void s_compute(const SWSlotR<R> &ws, const SASlotR<R>
         bf16x8 b[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
+            // zero-scale blocks hold sign-only codes in the packed copy (pack_kernel)
             const uint32_t e = (sc[t] >> (8 * ks)) & 0xffu;
-            // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
-            const uint32_t q = wv[t][ks] & (e == 0 ? 0x88888888u : 0xffffffffu);
-            b[t] = dequant8(q, e8m0_to_f32(e));
+            b[t] = dequant8(wv[t][ks], e8m0_to_f32(e));
         }
         const int uo = ((4 * ks + g) ^ n) * 16;
 #pragma unroll
@@ -2563,8 +2567,7 @@ __device__ __forceinline__ void s_compute_dyn(const SWSlotR<R> &ws, const SASlot
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const uint32_t e = (sc[t] >> (8 * ks)) & 0xffu;
-                const uint32_t q = wv[t][ks] & (e == 0 ? 0x88888888u : 0xffffffffu);
-                b[t] = dequant8(q, e8m0_to_f32(e));
+                b[t] = dequant8(wv[t][ks], e8m0_to_f32(e));  // zero scales: sign-only codes (pack_kernel)
             }
             const int uo = ((4 * ks + g) ^ n) * 16;
 #pragma unroll
@@ -2817,10 +2820,9 @@ __device__ __forceinline__ void s_k_step_mt(const SKReg<R, CT> &r, int ks, f32x4
     bf16x8 b[CT];
 #pragma unroll
     for (int t = 0; t < CT; ++t) {
+        // zero-scale blocks hold sign-only codes in the packed copy (pack_kernel)
         const uint32_t e = (r.sc[t / 2][t & 1] >> (8 * ks)) & 0xffu;
-        // e8m0 = 0 -> +-0 (code * 0.0 in the reference): keep only the sign bits
-        const uint32_t q = r.w[t / 2][t & 1] & (e == 0 ? 0x88888888u : 0xffffffffu);
-        b[t] = dequant8(q, e8m0_to_f32(e));
+        b[t] = dequant8(r.w[t / 2][t & 1], e8m0_to_f32(e));
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {

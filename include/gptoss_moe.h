@@ -268,8 +268,10 @@ int gptoss_moe_quantize_mxfp4(const float *src, int64_t n_elems, uint8_t *packed
  * Load-time weight packing (no counterpart in the reference, whose loader
  * converts weights once at start-up, getp_run.cpp:1041-1049): rearranges the
  * MXFP4 nibbles and e8m0 scales of w1 and w2 into MFMA fragment order for the
- * direct decode GEMM; byte values are unchanged, K is padded to a multiple of
- * 128 with zeros.  Run once per layer, keep the buffer and pass it as
+ * direct decode GEMM; byte values are unchanged except that the nibbles of a
+ * 32-element group whose e8m0 byte is 0 keep only their sign bits (their
+ * values are +-0 either way, as the reference's code * 0.0), K is padded to
+ * a multiple of 128 with zeros.  Run once per layer, keep the buffer and pass it as
  * weights.packed.  gptoss_moe_packed_size gives the buffer size (0 for an
  * invalid shape); the buffer must be 16-byte aligned.
  */

@@ -324,3 +324,40 @@ def test_slot_loads(R, rows):
         assert src.max() <= rows - 1
         slot[64 * h + LANE] = src
     assert np.array_equal(slot[:rows], np.arange(rows))
+
+
+def test_packed_zero_scale_groups_are_sign_only():
+    """pack_kernel / packing.pack_expected: a 32-element group whose e8m0
+    byte is 0 is stored with sign-only nibbles (values +-0 as the
+    reference's code * 0.0), every other byte unchanged; the e8m0 bytes
+    themselves are moved, not altered."""
+    from packing import pack_expected
+    rng = np.random.default_rng(3)
+    E, n, k = 2, 64, 384
+    wq = rng.integers(0, 256, E * n * k // 2, dtype=np.uint8)
+    ws = rng.integers(118, 130, E * n * k // 32, dtype=np.uint8)
+    zero = rng.random(ws.size) < 0.2
+    ws[zero] = 0
+    for mlp1 in (False, True):
+        got_w, got_s = pack_expected(wq, ws, n, k, mlp1)
+        ref_w, ref_s = pack_expected(wq, np.where(zero, 1, ws).astype(np.uint8), n, k, mlp1)
+        assert np.array_equal(np.sort(got_s), np.sort(np.concatenate(
+            [ws, np.zeros(got_s.size - ws.size, np.uint8)])))
+        changed = got_w != ref_w
+        assert np.array_equal(got_w[changed], ref_w[changed] & 0x88)  # only sign bits kept
+        # the masked bytes are exactly the zero groups' 16 bytes each
+        assert changed.sum() <= zero.sum() * 16
+        n_nz = int(((ref_w & 0x77) != 0).sum())
+        assert n_nz > 0
+        # every byte of a zero group has no magnitude bits left
+        src = np.arange(n)
+        if mlp1:
+            src = (src & ~31) + 2 * (src & 15) + ((src >> 4) & 1)
+        zg = zero.reshape(E, n, k // 32)[:, src]               # packed row order
+        zb = np.repeat(zg, 16, axis=2)                          # [E][n][k/2] bytes
+        kp = -(-k // 128)
+        zb_full = np.zeros((E, n, kp * 64), bool)
+        zb_full[:, :, :k // 2] = zb
+        zperm = zb_full.reshape(E, n // 16, 16, kp, 4, 4, 4).transpose(0, 1, 3, 5, 2, 4, 6).reshape(-1)
+        assert ((got_w[zperm] & 0x77) == 0).all()
+        assert np.array_equal(got_w[~zperm], ref_w[~zperm])
