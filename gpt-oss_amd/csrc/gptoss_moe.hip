@@ -61,6 +61,25 @@ __device__ __forceinline__ float bf16_round(float f) { return bf2f(f2bf(f)); }
 // e8m0 scale byte -> fp32 2^(e-127) (e = 0 -> 0.0), memory/mxfp4.hpp:53.
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) { return __uint_as_float(e << 23); }
 
+// e8m0_to_f32 of byte b of w in one VALU instruction (a byte-selected shift;
+// the compiler builds bytes 1..3 with a shift and a mask).  b is 0..3 and
+// folds to a constant where callers unroll.
+template <int B>
+__device__ __forceinline__ float e8m0_byte_to_f32_b(uint32_t w) {
+    uint32_t f;
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_%3"
+        : "=v"(f) : "v"(23u), "v"(w), "n"(B));
+    return __uint_as_float(f);
+}
+__device__ __forceinline__ float e8m0_byte_to_f32(uint32_t w, int b) {
+    switch (b) {
+        case 0: return e8m0_byte_to_f32_b<0>(w);
+        case 1: return e8m0_byte_to_f32_b<1>(w);
+        case 2: return e8m0_byte_to_f32_b<2>(w);
+        default: return e8m0_byte_to_f32_b<3>(w);
+    }
+}
+
 // 8 E2M1 codes (one dword, low nibble first) * scale -> 8 bf16.
 __device__ __forceinline__ bf16x8 dequant8(uint32_t q, float scale) {
     bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 0);
@@ -2530,8 +2549,7 @@ __device__ __forceinline__ void s_compute(const SWSlotR<R> &ws, const SASlotR<R>
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             // zero-scale blocks hold sign-only codes in the packed copy (pack_kernel)
-            const uint32_t e = (sc[t] >> (8 * ks)) & 0xffu;
-            b[t] = dequant8(wv[t][ks], e8m0_to_f32(e));
+            b[t] = dequant8(wv[t][ks], e8m0_byte_to_f32(sc[t], ks));
         }
         const int uo = ((4 * ks + g) ^ n) * 16;
 #pragma unroll
@@ -2821,8 +2839,7 @@ __device__ __forceinline__ void s_k_step_mt(const SKReg<R, CT> &r, int ks, f32x4
 #pragma unroll
     for (int t = 0; t < CT; ++t) {
         // zero-scale blocks hold sign-only codes in the packed copy (pack_kernel)
-        const uint32_t e = (r.sc[t / 2][t & 1] >> (8 * ks)) & 0xffu;
-        b[t] = dequant8(r.w[t / 2][t & 1], e8m0_to_f32(e));
+        b[t] = dequant8(r.w[t / 2][t & 1], e8m0_byte_to_f32(r.sc[t / 2][t & 1], ks));
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
