@@ -3979,6 +3979,8 @@ int gptoss_moe_forward_noalloc(const gptoss_moe_shape *shape, const gptoss_moe_w
                                const int32_t *forced_topk_i, const uint16_t *forced_topk_w,
                                unsigned flags, hipStream_t stream) {
     if (!shape_ok(shape) || n_tokens < 0) return GPTOSS_MOE_ERR_INVALID_ARG;
+    // the weight prefetch creates its side stream on first use: not here
+    if (flags & GPTOSS_MOE_FLAG_WEIGHT_PREFETCH) return GPTOSS_MOE_ERR_INVALID_ARG;
     // the workspace this call needs, laid out for exactly n_tokens
     const size_t need = ws_layout(*shape, n_tokens).total;
     if (need > kScratchBytes) return GPTOSS_MOE_ERR_WORKSPACE;

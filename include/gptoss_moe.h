@@ -199,6 +199,8 @@ int gptoss_moe_forward(const gptoss_moe_shape *shape, const gptoss_moe_weights *
  * shape, k = 4: up to about 1300 tokens).  Every call on one GPU shares its
  * array: calls that overlap on one GPU (different streams or host threads
  * without ordering) race.  Results equal gptoss_moe_forward's.
+ * GPTOSS_MOE_FLAG_WEIGHT_PREFETCH is rejected (GPTOSS_MOE_ERR_INVALID_ARG):
+ * its side stream is created on first use.
  */
 int gptoss_moe_forward_noalloc(const gptoss_moe_shape *shape, const gptoss_moe_weights *w,
                                const uint16_t *x_norm, uint16_t *out, int n_tokens,

@@ -123,6 +123,9 @@ def test_noalloc_rejects_without_gpu_work():
                                           None, None, 0, None) == gm.ERR_WORKSPACE
     assert lib.gptoss_moe_forward_noalloc(ctypes.byref(s20), ctypes.byref(w), None, None, -1,
                                           None, None, 0, None) == gm.ERR_INVALID_ARG
+    # the weight prefetch would create its side stream: rejected before any HIP call
+    assert lib.gptoss_moe_forward_noalloc(ctypes.byref(s20), ctypes.byref(w), None, None, 4,
+                                          None, None, gm.FLAG_WEIGHT_PREFETCH, None) == gm.ERR_INVALID_ARG
 
 
 def _fake_call(lib, shape, w, flags=0, n_tokens=0):
