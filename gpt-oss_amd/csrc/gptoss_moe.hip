@@ -2583,10 +2583,8 @@ __device__ __forceinline__ void s_compute_dyn(const SWSlotR<R> &ws, const SASlot
         if (ks < nks) {
             bf16x8 b[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint32_t e = (sc[t] >> (8 * ks)) & 0xffu;
-                b[t] = dequant8(wv[t][ks], e8m0_to_f32(e));  // zero scales: sign-only codes (pack_kernel)
-            }
+            for (int t = 0; t < 2; ++t)  // zero scales: sign-only codes (pack_kernel)
+                b[t] = dequant8(wv[t][ks], e8m0_byte_to_f32(sc[t], ks));
             const int uo = ((4 * ks + g) ^ n) * 16;
 #pragma unroll
             for (int m = 0; m < R / 16; ++m) {
