@@ -50,3 +50,29 @@ def test_cpu_baseline_reports_native_build_and_host(tmp_path):
     res = json.loads(r.stdout.strip().splitlines()[-1])
     assert res["kind"] == "port" and res["value"] > 0 and res["cores"] >= 1
     assert "march=native" in res["build"] and res["cpu"] != ""
+
+
+def test_variant_paths_and_flags_agree_with_the_header():
+    """The variant lines bench.py can time name paths that gptoss_moe knows,
+    and the flag expressions they record are the header's macros with the
+    values the Python binding passes."""
+    import ast
+    import re
+
+    import gptoss_moe as gm
+    src = open(os.path.join(ROOT, "bench.py")).read()
+    fn = src[src.index("def time_variants"):]
+    flags = ast.literal_eval(re.search(r"flags = (\{.*?\})\n", fn, re.S).group(1))
+    header = open(os.path.join(ROOT, "include", "gptoss_moe.h")).read()
+    macros = {m: int(v) for m, v in re.findall(r"#define (GPTOSS_MOE_FLAG_\w+) (\d+)u", header)}
+    for path, expr in flags.items():
+        assert path in gm._PATH_FLAGS, path
+        names = [n.strip() for n in expr.split("|")]
+        value = 0
+        for n in names:
+            assert n in macros, n
+            value |= macros[n]
+        assert value == gm._PATH_FLAGS[path], (path, value, gm._PATH_FLAGS[path])
+    # every FLAG_* constant of the binding is the header's value
+    for n, v in macros.items():
+        assert getattr(gm, n.replace("GPTOSS_MOE_", "")) == v, n
